@@ -1,0 +1,208 @@
+/*
+ * rstr_hip.h -- C ABI of librstr_hip.so, the MI355X (gfx950) backend of the
+ * pretrained-rstr resident continuous decode step.
+ *
+ * Plain pointers and sizes only.  Every call is synchronous with respect to the
+ * host buffers it is given (they may be reused on return), returns 0 on
+ * success or a negative RSTR_E_* status, and leaves a message readable with
+ * rstr_last_error().  No exception crosses the boundary.  A session is used by
+ * one host thread at a time (the reference's device-owning runtime thread,
+ * src/pretrained/continuation/paged_runtime.clj:4-5); its work is ordered on
+ * one in-order HIP stream, so a copy-on-write page copy issued before a step
+ * is complete before that step's append (paged_attention.clj:351-353).
+ *
+ * Each entry cites the reference interface it replaces (file:line into the
+ * reference repository).  INTEGRATION.md shows the JDK 21 FFM binding.
+ */
+#ifndef RSTR_HIP_H
+#define RSTR_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RSTR_OK 0
+#define RSTR_E_INVALID -1   /* argument or descriptor validation failed      */
+#define RSTR_E_HIP -2       /* a HIP runtime call failed                     */
+#define RSTR_E_OOM -3       /* device or host allocation failed              */
+#define RSTR_E_STATE -4     /* object closed or used out of order            */
+
+typedef struct rstr_session rstr_session;
+typedef struct rstr_model rstr_model;
+typedef struct rstr_pool rstr_pool;
+typedef struct rstr_decoder rstr_decoder;
+
+/* Descriptor flags of src/pretrained/arch/{gemma3,qwen3,llama}.clj plus the HF
+ * hyper-parameters read by decoder.clj:31-56 (load-hf). */
+typedef struct rstr_model_desc {
+  int32_t n_layers, d_model, d_ff, n_q, n_kv, head_dim, vocab;
+  int32_t weight_bits;        /* 4: Q4 block 32 + fp16 scale; 8: Q8 block 32   */
+  int32_t gain_offset;        /* 1: RMSNorm gain (1 + w) (gemma3.clj:29)        */
+  int32_t qk_norm;            /* per-head q/k RMSNorm                          */
+  int32_t sandwich;           /* post-attention and post-FFN norms             */
+  int32_t ffn_geglu;          /* 1: GELU(tanh) gate; 0: SiLU gate              */
+  int32_t rope_dual;          /* local/global RoPE theta per layer            */
+  int32_t global_pattern;     /* layer l is global iff (l+1) % p == 0; 0: all */
+  int32_t sliding_window;     /* local-layer window in tokens; 0: none        */
+  int32_t embed_scale_sqrt_d; /* embedding scaled by sqrt(d_model)            */
+  float eps;                  /* RMSNorm epsilon                               */
+  float attn_scale;           /* 1/sqrt(query_pre_attn_scalar or head_dim)    */
+  double rope_global, rope_local;
+} rstr_model_desc;
+
+/* Tensor roles (synthetic generator keys and host-tensor binding). */
+enum {
+  RSTR_ROLE_EMBED = 0, RSTR_ROLE_FINAL_NORM = 1, RSTR_ROLE_ATTN_NORM = 2, RSTR_ROLE_Q = 3,
+  RSTR_ROLE_K = 4, RSTR_ROLE_V = 5, RSTR_ROLE_O = 6, RSTR_ROLE_Q_NORM = 7, RSTR_ROLE_K_NORM = 8,
+  RSTR_ROLE_POST_ATTN_NORM = 9, RSTR_ROLE_FFN_PRE_NORM = 10, RSTR_ROLE_FFN_POST_NORM = 11,
+  RSTR_ROLE_GATE = 12, RSTR_ROLE_UP = 13, RSTR_ROLE_DOWN = 14
+};
+
+/* One host f32 tensor: linear weights row-major [out][in] (decoder.clj:77-86). */
+typedef struct rstr_tensor {
+  int32_t layer;   /* -1 for global tensors (embed, final norm) */
+  int32_t role;
+  const float* data;
+  int64_t elements;
+} rstr_tensor;
+
+/* ---- session --------------------------------------------------------------
+ * Replaces raster.gpu.core/make-session (decoder_gpu.clj:1103) and
+ * close-session! (continuation/model_worker.clj:35). */
+int rstr_session_open(int32_t device, rstr_session** out);
+int rstr_session_close(rstr_session* s);
+/* Replaces ex-info messages.  Valid until the next call on the session. */
+const char* rstr_last_error(const rstr_session* s);
+/* Message of the last failure of an open call that returned no session. */
+const char* rstr_open_error(void);
+
+/* ---- model binding ----------------------------------------------------------
+ * Replaces bind-decode! quantise + alloc + resident specs
+ * (decoder_gpu.clj:990-1131, specs :404-475, quantisation :36-54). */
+int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, const rstr_tensor* tensors,
+                    int32_t n_tensors, rstr_model** out);
+/* Same binding over seeded synthetic weights generated on the device
+ * (N(0,0.02) linears and embedding; norm gains N(0,0.02) around the gain
+ * offset, or 1+N(0,0.02)). */
+int rstr_model_bind_synthetic(rstr_session* s, const rstr_model_desc* desc, uint64_t seed,
+                              rstr_model** out);
+int rstr_model_close(rstr_model* m);
+/* Device bytes of the packed linear weights streamed by one decode step. */
+int64_t rstr_model_weight_bytes(const rstr_model* m);
+/* Download one quantised linear in the canonical packed layout: Q4 uint8
+ * [out][in/32][16] (byte j = q[2j] | q[2j+1] << 4), Q8 int8 [out][in/32][32];
+ * fp16 scales [out][in/32].  Used to check bit-exact quantisation. */
+int rstr_model_export_linear(rstr_model* m, int32_t layer, int32_t role, void* wq, uint16_t* ws);
+
+/* ---- page pool --------------------------------------------------------------
+ * Replaces page-pool/open-pool! device allocation (page_pool.clj:235-303):
+ * fp16 key and value slabs per layer, [page][page_size][n_kv][head_dim]. */
+int rstr_pool_open(rstr_model* m, int32_t page_size, int32_t physical_pages, rstr_pool** out);
+int rstr_pool_close(rstr_pool* p);
+/* Replaces copy-page! (page_pool.clj:892-900): one physical page of every
+ * slab and layer, ordered before later work on the session stream. */
+int rstr_pool_copy_page(rstr_pool* p, int32_t src_page, int32_t dst_page);
+/* Raw slab transfer of fp16 elements (gpu/upload! and gpu/download on a pool
+ * buffer key, page_pool.clj:284-293; the chunk restore/export staging). */
+int rstr_pool_upload(rstr_pool* p, int32_t slab, int32_t layer, int64_t dst_element,
+                     const uint16_t* src, int64_t elements);
+int rstr_pool_download(rstr_pool* p, int32_t slab, int32_t layer, int64_t src_element,
+                       uint16_t* dst, int64_t elements);
+/* Synthetic N(0,1) fp16 K/V in every layer of the listed pages, keyed by
+ * (seed, layer, slab, element): the stand-in for a restored prefix used by
+ * throughput runs.  No reference counterpart. */
+int rstr_pool_fill_synthetic(rstr_pool* p, const int32_t* pages, int32_t n_pages, uint64_t seed);
+
+/* ---- paged decoder ----------------------------------------------------------
+ * Replaces paged-decoder/open! (paged_decoder.clj:321-420) over a state bound
+ * with :cache-mode :paged and :batch-size `batch`.  `split` is the history
+ * tile (tokens, multiple of 4) of the split-K attention; it fixes the
+ * attention's reduction order and so is part of the numerics contract. */
+int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pages_per_seq,
+                      int32_t maxpos, int32_t split, rstr_decoder** out);
+int rstr_decoder_close(rstr_decoder* d);
+/* Replaces prime-lanes! -> upload-ranges! :r0 (paged_decoder.clj:462-471,
+ * decoder_gpu.clj:1248-1271): the prescaled embedding of each token becomes
+ * the lane's pending input row; other lanes keep their resident row. */
+int rstr_prime_lanes(rstr_decoder* d, int32_t n, const int32_t* lanes, const int32_t* tokens);
+/* Replaces decode-row! input upload (decoder_gpu.clj:1158-1170): arbitrary
+ * f32 rows [n][d_model] (the multimodal seam). */
+int rstr_prime_rows(rstr_decoder* d, int32_t n, const int32_t* lanes, const float* rows);
+/* Replaces step-lanes! upload-ranges! + gpu-link/run! + download :tokbuf
+ * (paged_decoder.clj:562-578).  Descriptors (int32): slots[batch] (physical
+ * slot page*page_size+offset, -1 = no append), row_offsets[batch+1] (0..batch),
+ * positions[batch], page_table[batch*pages_per_seq] (-1 padded),
+ * lengths[batch] (visible tokens including this step's row, 0 = inactive),
+ * start_positions[batch].  tokens_out[batch] receives the greedy next token of
+ * every lane; the next input row stays resident. */
+int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int32_t* row_offsets,
+                    const int32_t* positions, const int32_t* page_table, const int32_t* lengths,
+                    const int32_t* start_positions, int32_t* tokens_out);
+/* Logits [batch][vocab] of the last step (decode-row! returning logits,
+ * decoder_gpu.clj:1158-1170). */
+int rstr_decode_logits(rstr_decoder* d, float* logits_out);
+/* Resident input rows [batch][d_model] (the state :r0). */
+int rstr_decoder_read_rows(rstr_decoder* d, float* out);
+/* 1 (default): replay each step as one captured HIP graph; 0: launch eagerly. */
+int rstr_decoder_set_graph(rstr_decoder* d, int32_t enabled);
+
+/* ---- isolated routed append -------------------------------------------------
+ * Replaces the paged-append runner run! (paged_append.clj:179-339) over the
+ * routed append ABI (doc/serving-architecture.md:178-190): f32 rows
+ * k_rows/v_rows[batch][n_kv*head_dim] -> fp16, round to nearest even, at
+ * slot = page*page_size + offset; slot -1 skips the row.  Slots must be
+ * distinct. */
+int rstr_append_run(rstr_pool* p, int32_t layer, int32_t batch, const float* k_rows,
+                    const float* v_rows, const int32_t* slots);
+
+/* ---- isolated routed attention -----------------------------------------------
+ * Replaces paged-attention/run! (paged_attention.clj:322-474) with f32 query
+ * and output: q[batch][n_q][head_dim], one query row per sequence
+ * (row_offsets 0..batch), causal visibility with window-left = window-1
+ * (window 0 = none).  Reads layer `layer` of the pool. */
+int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                       int32_t window, float scale, const float* q, const int32_t* row_offsets,
+                       const int32_t* positions, const int32_t* page_table, int32_t pages_per_seq,
+                       const int32_t* lengths, const int32_t* start_positions, float* out);
+/* Timing form of rstr_attention_run: inputs uploaded once, `iters` launches
+ * timed with HIP events on the session stream; average ms per launch of the
+ * split kernel and of the merge kernel. */
+int rstr_attention_bench(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                         int32_t window, float scale, const float* q, const int32_t* page_table,
+                         int32_t pages_per_seq, const int32_t* lengths, int32_t iters,
+                         float* split_ms, float* merge_ms);
+
+/* ---- device-resident step schedules (measurement) ------------------------------
+ * A schedule is a list of steps whose descriptors (and the synthetic prefix
+ * fills and copy-on-write copies due before them) are uploaded ahead of time,
+ * so a run measures device work only.  No reference counterpart; the host
+ * bookkeeping that produced the descriptors is timed separately. */
+typedef struct rstr_staged_step {
+  const int32_t *slots, *row_offsets, *positions, *page_table, *lengths, *start_positions;
+  const int32_t* fill_pages;  /* pages to fill synthetically before the step */
+  int32_t n_fill;
+  uint64_t fill_seed;
+  const int32_t* cow_pairs;   /* (src, dst) page copies before the step */
+  int32_t n_cow;
+} rstr_staged_step;
+int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* steps, int32_t n_steps);
+/* Runs staged steps [first, first+count); tokens_out[count][batch]; device_ms
+ * = HIP-event time on the session stream. */
+int rstr_schedule_run(rstr_decoder* d, int32_t first, int32_t count, int32_t* tokens_out,
+                      float* device_ms);
+/* Kernel classes timed by rstr_decoder_profile_steps (eager launches with HIP
+ * events around each kernel). */
+enum {
+  RSTR_K_QGEMM = 0, RSTR_K_HEAD = 1, RSTR_K_ATTN_SPLIT = 2, RSTR_K_ATTN_MERGE = 3,
+  RSTR_K_QKV_POST = 4, RSTR_K_ROWS = 5, RSTR_K_TAIL = 6, RSTR_K_CLASSES = 7
+};
+/* Runs staged steps eagerly with per-kernel events; per class: total ms and
+ * launch count over the run. */
+int rstr_decoder_profile_steps(rstr_decoder* d, int32_t first, int32_t count, float* class_ms,
+                               int32_t* class_launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,915 @@
+/*
+ * rstr_oracle.c -- CPU restatement of the pretrained-rstr continuous decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY (see rstr_oracle.h).  Compiled with
+ * -ffp-contract=off: every multiply-add that is fused is written as fmaf().
+ *
+ * The canonical reduction orders fixed here are shared with the HIP kernels;
+ * they are this build's definition of the arithmetic, chosen so that the GPU
+ * decomposition (wavefront trees, split-K) reproduces them exactly.
+ */
+#include "rstr_oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static __thread char g_err[256];
+static void set_err(const char* msg) { snprintf(g_err, sizeof g_err, "%s", msg); }
+const char* orc_last_error(void) { return g_err; }
+
+static inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+static inline int32_t imax32(int32_t a, int32_t b) { return a > b ? a : b; }
+
+/* ------------------------------------------------------------------------ */
+/* fp16 <-> fp32.  Round to nearest even, the conversion the reference's     */
+/* routed append promises (doc/serving-architecture.md:178-190,              */
+/* paged_append.clj:179-228).  Pinned by tests against numpy.float16.       */
+/* ------------------------------------------------------------------------ */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u);     /* NaN -> quiet NaN   */
+  if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7C00u);    /* >= 65536 -> inf    */
+  if (ax >= 0x38800000u) {                                     /* f16 normal range   */
+    uint32_t mant = ax & 0x7FFFFFu;
+    uint32_t e = (ax >> 23) - 127u + 15u;
+    uint32_t h = (e << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;    /* may carry into inf */
+    return (uint16_t)(sign | h);
+  }
+  if (ax < 0x33000000u) return (uint16_t)sign;                 /* < 2^-25 -> 0       */
+  uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+  int e = (int)(ax >> 23) - 127;                               /* in [-25, -15]      */
+  int shift = -(e + 1);                                        /* in [14, 24]        */
+  uint32_t m = mant >> shift;
+  uint32_t rem = mant & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (m & 1u))) m++;
+  return (uint16_t)(sign | m);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t m = h & 0x3FFu;
+  uint32_t x;
+  if (e == 0) {
+    if (m == 0) {
+      x = sign;
+    } else { /* subnormal: normalise */
+      int sh = 0;
+      while (!(m & 0x400u)) { m <<= 1; sh++; }
+      m &= 0x3FFu;
+      x = sign | ((uint32_t)(127 - 15 + 1 - sh) << 23) | (m << 13);
+    }
+  } else if (e == 31) {
+    x = sign | 0x7F800000u | (m << 13);
+  } else {
+    x = sign | ((e - 15u + 127u) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+/* ------------------------------------------------------------------------ */
+/* exp: Cody-Waite reduction by ln2 (split hi/lo) and the degree-7 Taylor    */
+/* polynomial of e^r on |r| <= ln2/2, scaled by 2^n in two exact steps.      */
+/* Own implementation from the textbook method; pinned by tests against     */
+/* libm's double-precision exp (<= 2 ulp).                                   */
+/* ------------------------------------------------------------------------ */
+static inline float pow2i(int k) { /* k in [-126, 127] */
+  uint32_t x = (uint32_t)(k + 127) << 23;
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+float orc_exp(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e43p+6f) return INFINITY;        /* 88.7228...  */
+  if (x < -0x1.9fe36ap+6f) return 0.0f;           /* -103.972... */
+  float n = rintf(x * 0x1.715476p+0f);            /* x * log2(e) */
+  float r = fmaf(-n, 0x1.62e4p-1f, x);            /* ln2 hi (exact product) */
+  r = fmaf(-n, 0x1.7f7d1cp-20f, r);               /* ln2 lo */
+  float p = 0x1.a01a02p-13f;                      /* 1/5040 */
+  p = fmaf(p, r, 0x1.6c16c2p-10f);                /* 1/720  */
+  p = fmaf(p, r, 0x1.111112p-7f);                 /* 1/120  */
+  p = fmaf(p, r, 0x1.555556p-5f);                 /* 1/24   */
+  p = fmaf(p, r, 0x1.555556p-3f);                 /* 1/6    */
+  p = fmaf(p, r, 0x1.0p-1f);                      /* 1/2    */
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  int n1 = ni / 2;
+  int n2 = ni - n1;
+  return (p * pow2i(n1)) * pow2i(n2);
+}
+
+/* GELU, tanh form (Gemma's gelu_pytorch_tanh; decoder_gpu.clj:132 gelu-mul!). */
+float orc_gelu_tanh(float g) {
+  float g3 = (g * g) * g;
+  float u = 0x1.988454p-1f * (g + 0x1.6e4e26p-5f * g3); /* sqrt(2/pi), 0.044715 */
+  float e = orc_exp(u + u);
+  float t = 1.0f - 2.0f / (e + 1.0f);
+  return (0.5f * g) * (1.0f + t);
+}
+
+/* SiLU (silu-mul!, decoder_gpu.clj:132; decoder.clj:336-343). */
+float orc_silu(float g) { return g / (1.0f + orc_exp(-g)); }
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic weights: counter-based splitmix64, Irwin-Hall sum of twelve    */
+/* 16-bit uniforms (a classical N(0,1) approximation), all integer or exact */
+/* double arithmetic so CPU and GPU produce identical fp32 bits.             */
+/* ------------------------------------------------------------------------ */
+#define GOLDEN 0x9E3779B97F4A7C15ull
+
+uint64_t orc_splitmix64(uint64_t x) {
+  uint64_t z = x + GOLDEN;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint64_t orc_tensor_key(uint64_t seed, int32_t layer, int32_t role) {
+  uint64_t tag = ((uint64_t)(uint32_t)(layer + 1) << 16) | (uint64_t)(uint32_t)role;
+  return orc_splitmix64(orc_splitmix64(seed) ^ tag);
+}
+
+float orc_normal(uint64_t key, uint64_t index, double mean, double std) {
+  uint64_t s = 0;
+  for (int j = 0; j < 3; j++) {
+    uint64_t r = orc_splitmix64(key + (3u * index + (uint64_t)j) * GOLDEN);
+    s += (r & 0xFFFFu) + ((r >> 16) & 0xFFFFu) + ((r >> 32) & 0xFFFFu) + (r >> 48);
+  }
+  double v = ((double)s + 6.0) / 65536.0 - 6.0;
+  return (float)(mean + std * v);
+}
+
+void orc_normal_fill(uint64_t key, uint64_t start, int64_t n, double mean, double std, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) out[i] = orc_normal(key, start + (uint64_t)i, mean, std);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Block quantisation.  Q4: 32 weights per block, d = (signed max-magnitude) */
+/* / -8, q = min(15, trunc(w/d + 8.5)), d stored fp16 (the published GGML    */
+/* Q4_0 definition, the format the reference's CPU path names cq/q4-0 at     */
+/* decoder.clj:152-189).  Q8: d = max|w| / 127, q = rint(w/d)                */
+/* (decoder_gpu.clj:523-537 describes the same rule).  Rounding relative to  */
+/* Raster's packers: parity unpinned vs Raster.                              */
+/* Canonical packed layout: nib[row][block][16], byte j = q[2j] | q[2j+1]<<4.*/
+/* ------------------------------------------------------------------------ */
+static void quant_q4_block(const float* w, uint8_t* nib, uint16_t* scale) {
+  float amax = 0.0f, mx = 0.0f;
+  for (int i = 0; i < 32; i++) {
+    float a = fabsf(w[i]);
+    if (a > amax) { amax = a; mx = w[i]; }
+  }
+  float d = (amax > 0.0f) ? mx / -8.0f : 0.0f;   /* an all-zero block gets scale +0 */
+  float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  uint8_t q[32];
+  for (int i = 0; i < 32; i++) {
+    int v = (int)(w[i] * id + 8.5f);
+    q[i] = (uint8_t)(v > 15 ? 15 : v);
+  }
+  for (int j = 0; j < 16; j++) nib[j] = (uint8_t)(q[2 * j] | (q[2 * j + 1] << 4));
+  *scale = orc_f32_to_f16(d);
+}
+
+static void quant_q8_block(const float* w, int8_t* q, uint16_t* scale) {
+  float amax = 0.0f;
+  for (int i = 0; i < 32; i++) {
+    float a = fabsf(w[i]);
+    if (a > amax) amax = a;
+  }
+  float d = amax / 127.0f;
+  float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  for (int i = 0; i < 32; i++) {
+    int v = (int)rintf(w[i] * id);
+    q[i] = (int8_t)(v > 127 ? 127 : (v < -127 ? -127 : v));
+  }
+  *scale = orc_f32_to_f16(d);
+}
+
+void orc_quant_q4(const float* w, int64_t rows, int64_t cols, uint8_t* nib, uint16_t* scales) {
+  int64_t nb = cols / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t b = 0; b < nb; b++)
+      quant_q4_block(w + r * cols + 32 * b, nib + (r * nb + b) * 16, scales + r * nb + b);
+}
+
+void orc_quant_q8(const float* w, int64_t rows, int64_t cols, int8_t* q, uint16_t* scales) {
+  int64_t nb = cols / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t b = 0; b < nb; b++)
+      quant_q8_block(w + r * cols + 32 * b, q + (r * nb + b) * 32, scales + r * nb + b);
+}
+
+/* Activation quantisation, symmetric int8 per 32-element block with an fp32 */
+/* scale (the int8-quantised activation of qlinear-i8, decoder.clj:206-213;  */
+/* block size and rounding: parity unpinned vs Raster).                      */
+void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float* scales) {
+  int32_t nb = cols / 32;
+  for (int32_t r = 0; r < rows; r++) {
+    for (int32_t b = 0; b < nb; b++) {
+      const float* xb = x + (int64_t)r * cols + 32 * b;
+      float amax = 0.0f;
+      for (int i = 0; i < 32; i++) {
+        float a = fabsf(xb[i]);
+        if (a > amax) amax = a;
+      }
+      float d = amax / 127.0f;
+      float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+      for (int i = 0; i < 32; i++) {
+        int v = (int)rintf(xb[i] * id);
+        q[(int64_t)r * cols + 32 * b + i] = (int8_t)(v > 127 ? 127 : (v < -127 ? -127 : v));
+      }
+      scales[(int64_t)r * nb + b] = d;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dequantising linear y[r][n] = sum_b isum(r,n,b) * (dw[n,b] * dx[r,b]).    */
+/* Canonical order: the nb blocks form 64 contiguous parts of c=ceil(nb/64) */
+/* blocks (trailing parts may be short or empty); each part accumulates      */
+/* acc = fmaf(isum, dw*dx, acc) in block order from +0; the 64 part sums are */
+/* combined by the balanced pairwise tree in part order.  isum is the exact  */
+/* integer block dot.  Integer dots: pinned by brute force; the whole linear */
+/* is pinned against a float64 numpy restatement within 1e-5 relative.       */
+/* ------------------------------------------------------------------------ */
+static inline float tree64(float* v) {
+  for (int w = 1; w < 64; w <<= 1)
+    for (int i = 0; i < 64; i += 2 * w) v[i] = v[i] + v[i + w];
+  return v[0];
+}
+
+static inline int32_t dot_q4(const uint8_t* nib, const int8_t* x) {
+  int32_t s = 0;
+  for (int j = 0; j < 16; j++) {
+    int b = nib[j];
+    s += ((b & 15) - 8) * x[2 * j] + ((b >> 4) - 8) * x[2 * j + 1];
+  }
+  return s;
+}
+
+static inline int32_t dot_q8(const int8_t* q, const int8_t* x) {
+  int32_t s = 0;
+  for (int i = 0; i < 32; i++) s += (int32_t)q[i] * (int32_t)x[i];
+  return s;
+}
+
+void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out, int32_t k_in,
+                 const int8_t* xq, const float* xs, int32_t rows, float* y) {
+  int32_t nb = k_in / 32;
+  int32_t c = (nb + 63) / 64;
+#pragma omp parallel for schedule(static)
+  for (int32_t n = 0; n < n_out; n++) {
+    float dw[nb > 0 ? nb : 1];
+    for (int32_t b = 0; b < nb; b++) dw[b] = orc_f16_to_f32(ws[(int64_t)n * nb + b]);
+    for (int32_t r = 0; r < rows; r++) {
+      const int8_t* xr = xq + (int64_t)r * k_in;
+      const float* sr = xs + (int64_t)r * nb;
+      float part[64];
+      for (int32_t p = 0; p < 64; p++) {
+        float acc = 0.0f;
+        int32_t b0 = p * c;
+        int32_t b1 = (int32_t)imin64(nb, (int64_t)b0 + c);
+        for (int32_t b = b0; b < b1; b++) {
+          int32_t isum = (bits == 4)
+                             ? dot_q4((const uint8_t*)wq + ((int64_t)n * nb + b) * 16, xr + 32 * b)
+                             : dot_q8((const int8_t*)wq + ((int64_t)n * nb + b) * 32, xr + 32 * b);
+          float s = dw[b] * sr[b];
+          acc = fmaf((float)isum, s, acc);
+        }
+        part[p] = acc;
+      }
+      y[(int64_t)r * n_out + n] = tree64(part);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm y = (x * r) * (goff + g), r = 1/sqrt(mean(x^2) + eps)             */
+/* (nn/rms-norm!, decoder_gpu.clj:134-137; decoder.clj:295-300).            */
+/* Canonical sum of squares: element i goes to slot (i/4) mod 64, each slot  */
+/* accumulates fmaf(x,x,acc) in index order, slots combine by the pairwise   */
+/* tree.  Pinned by closed forms and by a float64 numpy restatement.         */
+/* ------------------------------------------------------------------------ */
+float orc_sumsq(const float* x, int32_t n) {
+  float slot[64];
+  for (int i = 0; i < 64; i++) slot[i] = 0.0f;
+  for (int32_t i = 0; i < n; i++) {
+    int s = (i >> 2) & 63;
+    slot[s] = fmaf(x[i], x[i], slot[s]);
+  }
+  return tree64(slot);
+}
+
+void orc_rmsnorm(const float* x, const float* g, float gain_offset, float eps, int32_t rows,
+                 int32_t n, float* y) {
+  for (int32_t r = 0; r < rows; r++) {
+    const float* xr = x + (int64_t)r * n;
+    float ss = orc_sumsq(xr, n);
+    float mean = ss / (float)n;
+    float rr = 1.0f / sqrtf(mean + eps);
+    for (int32_t i = 0; i < n; i++) y[(int64_t)r * n + i] = (xr[i] * rr) * (gain_offset + g[i]);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE, HF rotate-half pairing (attn/rope-pos-rows-buf!,                    */
+/* decoder_gpu.clj:177-178; theta per layer :477-488).  Angles in double,    */
+/* rounded to float tables; pinned by rotation invariants in tests.          */
+/* ------------------------------------------------------------------------ */
+void orc_rope_table(double theta, int32_t head_dim, int32_t maxpos, float* cos_t, float* sin_t) {
+  int32_t half = head_dim / 2;
+  for (int32_t p = 0; p < maxpos; p++)
+    for (int32_t i = 0; i < half; i++) {
+      double inv = pow(theta, -(2.0 * (double)i) / (double)head_dim);
+      double ang = (double)p * inv;
+      cos_t[(int64_t)p * half + i] = (float)cos(ang);
+      sin_t[(int64_t)p * half + i] = (float)sin(ang);
+    }
+}
+
+void orc_rope(const float* x, int32_t rows, int32_t heads, int32_t head_dim, const int32_t* pos,
+              const float* cos_t, const float* sin_t, float* y) {
+  int32_t half = head_dim / 2;
+  for (int32_t r = 0; r < rows; r++) {
+    const float* ct = cos_t + (int64_t)pos[r] * half;
+    const float* st = sin_t + (int64_t)pos[r] * half;
+    for (int32_t h = 0; h < heads; h++) {
+      const float* xh = x + ((int64_t)r * heads + h) * head_dim;
+      float* yh = y + ((int64_t)r * heads + h) * head_dim;
+      for (int32_t i = 0; i < half; i++) {
+        float a = xh[i], b = xh[i + half], c = ct[i], s = st[i];
+        yh[i] = (a * c) - (b * s);
+        yh[i + half] = (b * c) + (a * s);
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Paged attention decode (paged_attention.clj:196-228: fp16 K/V pages       */
+/* [page][page_size][n_kv][hd], f32 query/output/accumulator; visibility     */
+/* paged_decoder.clj:166-177, window-left = window-1).                       */
+/* Canonical order:                                                          */
+/*  dot(q,k): dims form 8-wide chunks; chunk c belongs to slice c mod 16;    */
+/*    each slice accumulates fmaf(q,k,acc) in dim order; slices combine as   */
+/*    v8[i]=s[i]+s[i+8], v4[i]=v8[i]+v8[i+4], v2[i]=v4[i]+v4[i+2], v2[0]+v2[1].*/
+/*    score = dot * scale.                                                   */
+/*  history: route-relative token t; splits cover [kS,(k+1)S) of the visible */
+/*    range.  Per split: m = max score; p = exp(score-m); token t adds to    */
+/*    group t mod 4 (l_g += p, o_g = fmaf(p, v, o_g)) in token order; groups */
+/*    combine ((g0+g1)+(g2+g3)).                                             */
+/*  merge: M = max m_k; in split order w = exp(m_k-M), L = fmaf(l_k,w,L),    */
+/*    O = fmaf(o_k,w,O); out = O / L.  Empty route: out = 0.                 */
+/* Pinned by the reference KATs (continuation_paged_attention_device_test    */
+/* .clj:42-174) and a float64 numpy softmax on random inputs.                */
+/* ------------------------------------------------------------------------ */
+static inline float kv_at(const void* base, int32_t f16, int64_t idx) {
+  return f16 ? orc_f16_to_f32(((const uint16_t*)base)[idx]) : ((const float*)base)[idx];
+}
+
+float orc_dot_canon(const float* q, const void* k, int32_t k_f16, int32_t hd) {
+  float s[16];
+  for (int i = 0; i < 16; i++) s[i] = 0.0f;
+  int32_t nch = hd / 8;
+  for (int32_t c = 0; c < nch; c++) {
+    int sl = c & 15;
+    for (int e = 0; e < 8; e++) {
+      int32_t d = c * 8 + e;
+      s[sl] = fmaf(q[d], kv_at(k, k_f16, d), s[sl]);
+    }
+  }
+  float v8[8], v4[4], v2[2];
+  for (int i = 0; i < 8; i++) v8[i] = s[i] + s[i + 8];
+  for (int i = 0; i < 4; i++) v4[i] = v8[i] + v8[i + 4];
+  for (int i = 0; i < 2; i++) v2[i] = v4[i] + v4[i + 2];
+  return v2[0] + v2[1];
+}
+
+void orc_attention(const float* q, const void* kpages, const void* vpages, int32_t kv_f16,
+                   int32_t page_size, int32_t n_kv, int32_t hd, int32_t n_q, int32_t batch,
+                   const int32_t* page_table, int32_t pps, const int32_t* lengths, int32_t window,
+                   float scale, int32_t split, float* out) {
+  int32_t group = n_q / n_kv;
+  int64_t esz = kv_f16 ? 2 : 4;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int32_t b = 0; b < batch; b++) {
+    for (int32_t h = 0; h < n_q; h++) {
+      float* o = out + ((int64_t)b * n_q + h) * hd;
+      int32_t len = lengths[b];
+      if (len <= 0) {
+        for (int32_t d = 0; d < hd; d++) o[d] = 0.0f;
+        continue;
+      }
+      const float* qh = q + ((int64_t)b * n_q + h) * hd;
+      int32_t kvh = h / group;
+      int32_t lo = 0, hi = len;
+      if (window > 0) lo = imax32(0, len - window);
+      int32_t k0 = lo / split, k1 = (hi - 1) / split;
+      int32_t nsplit = k1 - k0 + 1;
+      float* ms = (float*)malloc(sizeof(float) * (size_t)nsplit);
+      float* ls = (float*)malloc(sizeof(float) * (size_t)nsplit);
+      float* os = (float*)malloc(sizeof(float) * (size_t)nsplit * (size_t)hd);
+      float* sc = (float*)malloc(sizeof(float) * (size_t)split);
+      float* og = (float*)malloc(sizeof(float) * 4 * (size_t)hd);
+      for (int32_t k = k0; k <= k1; k++) {
+        int32_t t0 = lo > k * split ? lo : k * split;
+        int32_t t1 = hi < (k + 1) * split ? hi : (k + 1) * split;
+        float m = -INFINITY;
+        for (int32_t t = t0; t < t1; t++) {
+          int32_t page = page_table[(int64_t)b * pps + t / page_size];
+          int64_t row = (((int64_t)page * page_size + t % page_size) * n_kv + kvh) * hd;
+          const char* kr = (const char*)kpages + row * esz;
+          float s = orc_dot_canon(qh, kr, kv_f16, hd) * scale;
+          sc[t - t0] = s;
+          if (s > m) m = s;
+        }
+        float lg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 4 * hd; i++) og[i] = 0.0f;
+        for (int32_t t = t0; t < t1; t++) {
+          int32_t page = page_table[(int64_t)b * pps + t / page_size];
+          int64_t row = (((int64_t)page * page_size + t % page_size) * n_kv + kvh) * hd;
+          float p = orc_exp(sc[t - t0] - m);
+          int g = t & 3;
+          lg[g] = lg[g] + p;
+          for (int32_t d = 0; d < hd; d++)
+            og[g * hd + d] = fmaf(p, kv_at(vpages, kv_f16, row + d), og[g * hd + d]);
+        }
+        int32_t ki = k - k0;
+        ms[ki] = m;
+        ls[ki] = (lg[0] + lg[1]) + (lg[2] + lg[3]);
+        for (int32_t d = 0; d < hd; d++)
+          os[(int64_t)ki * hd + d] =
+              (og[d] + og[hd + d]) + (og[2 * hd + d] + og[3 * hd + d]);
+      }
+      float M = -INFINITY;
+      for (int32_t ki = 0; ki < nsplit; ki++)
+        if (ms[ki] > M) M = ms[ki];
+      float L = 0.0f;
+      for (int32_t d = 0; d < hd; d++) o[d] = 0.0f;
+      for (int32_t ki = 0; ki < nsplit; ki++) {
+        float w = orc_exp(ms[ki] - M);
+        L = fmaf(ls[ki], w, L);
+        for (int32_t d = 0; d < hd; d++) o[d] = fmaf(os[(int64_t)ki * hd + d], w, o[d]);
+      }
+      for (int32_t d = 0; d < hd; d++) o[d] = o[d] / L;
+      free(ms); free(ls); free(os); free(sc); free(og);
+    }
+  }
+}
+
+/* Argmax per row: ties take the lowest id, NaN beats every finite value and */
+/* the lowest NaN id wins (decoder_gpu.clj:64-71; KAT                        */
+/* decoder_gpu_composition_test.clj:9-20).                                   */
+void orc_argmax_rows(const float* logits, int32_t rows, int32_t vocab, int32_t* out) {
+  for (int32_t r = 0; r < rows; r++) {
+    const float* l = logits + (int64_t)r * vocab;
+    int32_t best = 0;
+    float bv = l[0];
+    for (int32_t i = 1; i < vocab; i++) {
+      float v = l[i];
+      if (bv != bv) break;            /* a NaN at best: nothing later beats it */
+      if (v != v || v > bv) { best = i; bv = v; }
+    }
+    out[r] = best;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Model: synthetic seeded weights (N(0,0.02) linears and embedding; norm   */
+/* gains N(0,0.02) with a +1 gain offset, else 1+N(0,0.02)), quantised to    */
+/* the canonical packed layout.                                             */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  void* wq;      /* Q4: uint8[n][nb][16]; Q8: int8[n][nb][32] */
+  uint16_t* ws;  /* fp16 scales [n][nb] */
+  int32_t n, k;
+} qtensor;
+
+typedef struct {
+  float *attn_norm, *q_norm, *k_norm, *post_attn_norm, *ffn_pre_norm, *ffn_post_norm;
+  qtensor q, k, v, o, gate, up, down;
+} layer_w;
+
+struct orc_model {
+  orc_desc d;
+  uint64_t seed;
+  layer_w* layers;
+  qtensor head;      /* tied embedding, quantised */
+  float* final_norm;
+  float* rope_cos[2];
+  float* rope_sin[2];
+  int32_t rope_maxpos;
+};
+
+static int64_t qbytes(int32_t bits, int32_t n, int32_t k) {
+  return (int64_t)n * (k / 32) * (bits == 4 ? 16 : 32);
+}
+
+static void make_linear(orc_model* m, int32_t layer, int32_t role, int32_t n, int32_t k, qtensor* t) {
+  int32_t bits = m->d.weight_bits;
+  t->n = n;
+  t->k = k;
+  t->wq = malloc((size_t)qbytes(bits, n, k));
+  t->ws = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)n * (size_t)(k / 32));
+  uint64_t key = orc_tensor_key(m->seed, layer, role);
+  int64_t nb = k / 32;
+#pragma omp parallel for schedule(static)
+  for (int32_t r = 0; r < n; r++) {
+    float w[32];
+    for (int64_t b = 0; b < nb; b++) {
+      uint64_t base = (uint64_t)r * (uint64_t)k + (uint64_t)(32 * b);
+      for (int i = 0; i < 32; i++) w[i] = orc_normal(key, base + (uint64_t)i, 0.0, 0.02);
+      if (bits == 4)
+        quant_q4_block(w, (uint8_t*)t->wq + ((int64_t)r * nb + b) * 16, t->ws + (int64_t)r * nb + b);
+      else
+        quant_q8_block(w, (int8_t*)t->wq + ((int64_t)r * nb + b) * 32, t->ws + (int64_t)r * nb + b);
+    }
+  }
+}
+
+static float* make_norm(orc_model* m, int32_t layer, int32_t role, int32_t n) {
+  float* g = (float*)malloc(sizeof(float) * (size_t)n);
+  double mean = m->d.gain_offset ? 0.0 : 1.0;
+  orc_normal_fill(orc_tensor_key(m->seed, layer, role), 0, n, mean, 0.02, g);
+  return g;
+}
+
+static int desc_ok(const orc_desc* d) {
+  if (d->n_layers <= 0 || d->d_model <= 0 || d->d_ff <= 0 || d->n_q <= 0 || d->n_kv <= 0 ||
+      d->head_dim <= 0 || d->vocab <= 0)
+    return 0;
+  if (d->d_model % 32 || d->d_ff % 32 || (d->n_q * d->head_dim) % 32 || d->head_dim % 8 ||
+      (d->head_dim & 1) || d->n_q % d->n_kv)
+    return 0;
+  if (d->weight_bits != 4 && d->weight_bits != 8) return 0;
+  return 1;
+}
+
+orc_model* orc_model_synthetic(const orc_desc* desc, uint64_t seed) {
+  if (!desc_ok(desc)) {
+    set_err("invalid model descriptor");
+    return NULL;
+  }
+  orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+  m->d = *desc;
+  m->seed = seed;
+  int32_t d = desc->d_model, qd = desc->n_q * desc->head_dim, kvr = desc->n_kv * desc->head_dim;
+  m->layers = (layer_w*)calloc((size_t)desc->n_layers, sizeof(layer_w));
+  for (int32_t l = 0; l < desc->n_layers; l++) {
+    layer_w* L = &m->layers[l];
+    L->attn_norm = make_norm(m, l, ORC_ROLE_ATTN_NORM, d);
+    L->ffn_pre_norm = make_norm(m, l, ORC_ROLE_FFN_PRE_NORM, d);
+    if (desc->qk_norm) {
+      L->q_norm = make_norm(m, l, ORC_ROLE_Q_NORM, desc->head_dim);
+      L->k_norm = make_norm(m, l, ORC_ROLE_K_NORM, desc->head_dim);
+    }
+    if (desc->sandwich) {
+      L->post_attn_norm = make_norm(m, l, ORC_ROLE_POST_ATTN_NORM, d);
+      L->ffn_post_norm = make_norm(m, l, ORC_ROLE_FFN_POST_NORM, d);
+    }
+    make_linear(m, l, ORC_ROLE_Q, qd, d, &L->q);
+    make_linear(m, l, ORC_ROLE_K, kvr, d, &L->k);
+    make_linear(m, l, ORC_ROLE_V, kvr, d, &L->v);
+    make_linear(m, l, ORC_ROLE_O, d, qd, &L->o);
+    make_linear(m, l, ORC_ROLE_GATE, desc->d_ff, d, &L->gate);
+    make_linear(m, l, ORC_ROLE_UP, desc->d_ff, d, &L->up);
+    make_linear(m, l, ORC_ROLE_DOWN, d, desc->d_ff, &L->down);
+  }
+  make_linear(m, -1, ORC_ROLE_EMBED, desc->vocab, d, &m->head);
+  m->final_norm = make_norm(m, -1, ORC_ROLE_FINAL_NORM, d);
+  return m;
+}
+
+static void free_q(qtensor* t) { free(t->wq); free(t->ws); }
+
+void orc_model_free(orc_model* m) {
+  if (!m) return;
+  for (int32_t l = 0; l < m->d.n_layers; l++) {
+    layer_w* L = &m->layers[l];
+    free(L->attn_norm); free(L->ffn_pre_norm); free(L->q_norm); free(L->k_norm);
+    free(L->post_attn_norm); free(L->ffn_post_norm);
+    free_q(&L->q); free_q(&L->k); free_q(&L->v); free_q(&L->o);
+    free_q(&L->gate); free_q(&L->up); free_q(&L->down);
+  }
+  free(m->layers);
+  free_q(&m->head);
+  free(m->final_norm);
+  for (int i = 0; i < 2; i++) { free(m->rope_cos[i]); free(m->rope_sin[i]); }
+  free(m);
+}
+
+static const qtensor* find_linear(const orc_model* m, int32_t layer, int32_t role) {
+  if (role == ORC_ROLE_EMBED) return &m->head;
+  if (layer < 0 || layer >= m->d.n_layers) return NULL;
+  const layer_w* L = &m->layers[layer];
+  switch (role) {
+    case ORC_ROLE_Q: return &L->q;
+    case ORC_ROLE_K: return &L->k;
+    case ORC_ROLE_V: return &L->v;
+    case ORC_ROLE_O: return &L->o;
+    case ORC_ROLE_GATE: return &L->gate;
+    case ORC_ROLE_UP: return &L->up;
+    case ORC_ROLE_DOWN: return &L->down;
+    default: return NULL;
+  }
+}
+
+int64_t orc_model_tensor(const orc_model* m, int32_t layer, int32_t role, void* wq, uint16_t* ws) {
+  const qtensor* t = find_linear(m, layer, role);
+  if (!t) return -1;
+  int64_t nbytes = qbytes(m->d.weight_bits, t->n, t->k);
+  if (wq) memcpy(wq, t->wq, (size_t)nbytes);
+  if (ws) memcpy(ws, t->ws, sizeof(uint16_t) * (size_t)t->n * (size_t)(t->k / 32));
+  return nbytes;
+}
+
+int64_t orc_model_norm(const orc_model* m, int32_t layer, int32_t role, float* out) {
+  const float* g = NULL;
+  int32_t n = m->d.d_model;
+  if (role == ORC_ROLE_FINAL_NORM) {
+    g = m->final_norm;
+  } else if (layer >= 0 && layer < m->d.n_layers) {
+    const layer_w* L = &m->layers[layer];
+    switch (role) {
+      case ORC_ROLE_ATTN_NORM: g = L->attn_norm; break;
+      case ORC_ROLE_FFN_PRE_NORM: g = L->ffn_pre_norm; break;
+      case ORC_ROLE_POST_ATTN_NORM: g = L->post_attn_norm; break;
+      case ORC_ROLE_FFN_POST_NORM: g = L->ffn_post_norm; break;
+      case ORC_ROLE_Q_NORM: g = L->q_norm; n = m->d.head_dim; break;
+      case ORC_ROLE_K_NORM: g = L->k_norm; n = m->d.head_dim; break;
+      default: break;
+    }
+  }
+  if (!g) return -1;
+  if (out) memcpy(out, g, sizeof(float) * (size_t)n);
+  return n;
+}
+
+/* Embedding row prescaled in double (decoder_gpu.clj:80-91 prescaled-embed, */
+/* embed-row :500-505): (float)(sqrt(d) * (double)e) or e.                   */
+void orc_embed_row(const orc_model* m, int32_t token, float* out) {
+  int32_t d = m->d.d_model;
+  uint64_t key = orc_tensor_key(m->seed, -1, ORC_ROLE_EMBED);
+  double scale = m->d.embed_scale_sqrt_d ? sqrt((double)d) : 1.0;
+  for (int32_t j = 0; j < d; j++) {
+    float e = orc_normal(key, (uint64_t)token * (uint64_t)d + (uint64_t)j, 0.0, 0.02);
+    out[j] = m->d.embed_scale_sqrt_d ? (float)(scale * (double)e) : e;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Paged decoder: the lane-step ABI of paged_decoder.clj:512-583 over a      */
+/* page pool [page][page_size][n_kv][hd] per layer and slab.                  */
+/* ------------------------------------------------------------------------ */
+struct orc_decoder {
+  const orc_model* m;
+  int32_t batch, page_size, physical_pages, pps, maxpos, kv_f16, split;
+  void** kslab;
+  void** vslab;
+  float *r0, *logits;
+  float* rope_cos[2];
+  float* rope_sin[2];
+};
+
+static int global_layer(const orc_desc* d, int32_t l) {
+  if (d->global_pattern <= 0) return 1;
+  return ((l + 1) % d->global_pattern) == 0;
+}
+
+orc_decoder* orc_decoder_open(const orc_model* m, int32_t batch, int32_t page_size,
+                              int32_t physical_pages, int32_t pages_per_seq, int32_t maxpos,
+                              int32_t kv_f16, int32_t split) {
+  if (batch <= 0 || page_size <= 0 || physical_pages <= 0 || pages_per_seq <= 0 || maxpos <= 0 ||
+      split <= 0 || split % 4) {
+    set_err("invalid decoder geometry");
+    return NULL;
+  }
+  orc_decoder* d = (orc_decoder*)calloc(1, sizeof(orc_decoder));
+  d->m = m;
+  d->batch = batch;
+  d->page_size = page_size;
+  d->physical_pages = physical_pages;
+  d->pps = pages_per_seq;
+  d->maxpos = maxpos;
+  d->kv_f16 = kv_f16;
+  d->split = split;
+  int32_t L = m->d.n_layers;
+  int64_t elems = (int64_t)physical_pages * page_size * m->d.n_kv * m->d.head_dim;
+  int64_t esz = kv_f16 ? 2 : 4;
+  d->kslab = (void**)calloc((size_t)L, sizeof(void*));
+  d->vslab = (void**)calloc((size_t)L, sizeof(void*));
+  for (int32_t l = 0; l < L; l++) {
+    d->kslab[l] = calloc((size_t)elems, (size_t)esz);
+    d->vslab[l] = calloc((size_t)elems, (size_t)esz);
+  }
+  d->r0 = (float*)calloc((size_t)batch * (size_t)m->d.d_model, sizeof(float));
+  d->logits = (float*)calloc((size_t)batch * (size_t)m->d.vocab, sizeof(float));
+  int32_t half = m->d.head_dim / 2;
+  for (int i = 0; i < 2; i++) {
+    double theta = (i == 0) ? m->d.rope_global : m->d.rope_local;
+    d->rope_cos[i] = (float*)malloc(sizeof(float) * (size_t)maxpos * (size_t)half);
+    d->rope_sin[i] = (float*)malloc(sizeof(float) * (size_t)maxpos * (size_t)half);
+    orc_rope_table(theta, m->d.head_dim, maxpos, d->rope_cos[i], d->rope_sin[i]);
+  }
+  return d;
+}
+
+void orc_decoder_free(orc_decoder* d) {
+  if (!d) return;
+  for (int32_t l = 0; l < d->m->d.n_layers; l++) { free(d->kslab[l]); free(d->vslab[l]); }
+  free(d->kslab); free(d->vslab); free(d->r0); free(d->logits);
+  for (int i = 0; i < 2; i++) { free(d->rope_cos[i]); free(d->rope_sin[i]); }
+  free(d);
+}
+
+void orc_prime_lanes(orc_decoder* d, int32_t n, const int32_t* lanes, const int32_t* tokens) {
+  for (int32_t i = 0; i < n; i++)
+    orc_embed_row(d->m, tokens[i], d->r0 + (int64_t)lanes[i] * d->m->d.d_model);
+}
+
+const float* orc_logits(const orc_decoder* d) { return d->logits; }
+const float* orc_r0(const orc_decoder* d) { return d->r0; }
+void* orc_slab(orc_decoder* d, int32_t slab, int32_t layer) {
+  return slab == 0 ? d->kslab[layer] : d->vslab[layer];
+}
+
+void orc_copy_page(orc_decoder* d, int32_t src, int32_t dst) {
+  int64_t pe = (int64_t)d->page_size * d->m->d.n_kv * d->m->d.head_dim;
+  int64_t esz = d->kv_f16 ? 2 : 4;
+  for (int32_t l = 0; l < d->m->d.n_layers; l++) {
+    memcpy((char*)d->kslab[l] + dst * pe * esz, (char*)d->kslab[l] + src * pe * esz, (size_t)(pe * esz));
+    memcpy((char*)d->vslab[l] + dst * pe * esz, (char*)d->vslab[l] + src * pe * esz, (size_t)(pe * esz));
+  }
+}
+
+/* Synthetic N(0,1) K/V for one physical page in every layer: the stand-in  */
+/* for a restored prefix used by the throughput configurations.             */
+void orc_fill_synthetic(orc_decoder* d, int32_t page, uint64_t seed) {
+  int64_t pe = (int64_t)d->page_size * d->m->d.n_kv * d->m->d.head_dim;
+  for (int32_t l = 0; l < d->m->d.n_layers; l++) {
+    for (int s = 0; s < 2; s++) {
+      uint64_t key = orc_tensor_key(seed, l, 64 + s);
+      void* slab = s == 0 ? d->kslab[l] : d->vslab[l];
+      for (int64_t e = 0; e < pe; e++) {
+        uint64_t idx = (uint64_t)page * (uint64_t)pe + (uint64_t)e;
+        float v = orc_normal(key, idx, 0.0, 1.0);
+        if (d->kv_f16)
+          ((uint16_t*)slab)[idx] = orc_f32_to_f16(v);
+        else
+          ((float*)slab)[idx] = v;
+      }
+    }
+  }
+}
+
+static int validate_step(const orc_decoder* d, const int32_t* slots, const int32_t* row_offsets,
+                         const int32_t* positions, const int32_t* page_table,
+                         const int32_t* lengths, const int32_t* starts) {
+  int64_t slot_limit = (int64_t)d->physical_pages * d->page_size;
+  for (int32_t b = 0; b <= d->batch; b++)
+    if (row_offsets[b] != b) { set_err("row offsets must be 0..batch for decode"); return 0; }
+  for (int32_t b = 0; b < d->batch; b++) {
+    int32_t len = lengths[b];
+    if (len < 0 || (int64_t)len > (int64_t)d->pps * d->page_size) { set_err("lane length out of range"); return 0; }
+    if (slots[b] < -1 || slots[b] >= slot_limit) { set_err("append slot out of range"); return 0; }
+    if (len == 0) {
+      if (slots[b] != -1) { set_err("inactive lane has an append slot"); return 0; }
+      continue;
+    }
+    if (positions[b] != starts[b] + len - 1 || positions[b] < 0 || positions[b] >= d->maxpos) {
+      set_err("query position must be the route's last visible token"); return 0;
+    }
+    int32_t np = (len + d->page_size - 1) / d->page_size;
+    for (int32_t p = 0; p < np; p++) {
+      int32_t pg = page_table[(int64_t)b * d->pps + p];
+      if (pg < 0 || pg >= d->physical_pages) { set_err("page table entry out of range"); return 0; }
+    }
+    if (slots[b] >= 0) {
+      int32_t t = len - 1;
+      int64_t want = (int64_t)page_table[(int64_t)b * d->pps + t / d->page_size] * d->page_size +
+                     t % d->page_size;
+      if (want != slots[b]) { set_err("append slot is not the route's last token"); return 0; }
+    }
+  }
+  return 1;
+}
+
+static void rows_qlinear(const orc_model* m, const qtensor* t, const float* x, int32_t rows, float* y) {
+  int32_t k = t->k, nb = k / 32;
+  int8_t* xq = (int8_t*)malloc((size_t)rows * (size_t)k);
+  float* xs = (float*)malloc(sizeof(float) * (size_t)rows * (size_t)nb);
+  orc_quant_act(x, rows, k, xq, xs);
+  orc_qlinear(m->d.weight_bits, t->wq, t->ws, t->n, k, xq, xs, rows, y);
+  free(xq);
+  free(xs);
+}
+
+int32_t orc_step_lanes(orc_decoder* d, const int32_t* slots, const int32_t* row_offsets,
+                       const int32_t* positions, const int32_t* page_table,
+                       const int32_t* lengths, const int32_t* start_positions,
+                       int32_t* tokens_out) {
+  if (!validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions))
+    return -1;
+  const orc_model* m = d->m;
+  const orc_desc* D = &m->d;
+  int32_t B = d->batch, dm = D->d_model, hd = D->head_dim, nq = D->n_q, nkv = D->n_kv;
+  int32_t qd = nq * hd, kvr = nkv * hd, ff = D->d_ff;
+  float goff = D->gain_offset ? 1.0f : 0.0f;
+  float* x = (float*)malloc(sizeof(float) * (size_t)B * dm);
+  float* h = (float*)malloc(sizeof(float) * (size_t)B * dm);
+  float* q = (float*)malloc(sizeof(float) * (size_t)B * qd);
+  float* k = (float*)malloc(sizeof(float) * (size_t)B * kvr);
+  float* v = (float*)malloc(sizeof(float) * (size_t)B * kvr);
+  float* qn = (float*)malloc(sizeof(float) * (size_t)B * qd);
+  float* kn = (float*)malloc(sizeof(float) * (size_t)B * kvr);
+  float* at = (float*)malloc(sizeof(float) * (size_t)B * qd);
+  float* o = (float*)malloc(sizeof(float) * (size_t)B * dm);
+  float* o2 = (float*)malloc(sizeof(float) * (size_t)B * dm);
+  float* g = (float*)malloc(sizeof(float) * (size_t)B * ff);
+  float* u = (float*)malloc(sizeof(float) * (size_t)B * ff);
+  memcpy(x, d->r0, sizeof(float) * (size_t)B * dm);
+  int64_t esz = d->kv_f16 ? 2 : 4;
+  for (int32_t l = 0; l < D->n_layers; l++) {
+    const layer_w* L = &m->layers[l];
+    int glob = global_layer(D, l);
+    int ti = (D->rope_dual && !glob) ? 1 : 0;
+    int32_t window = (D->sliding_window > 0 && !glob) ? D->sliding_window : 0;
+    orc_rmsnorm(x, L->attn_norm, goff, D->eps, B, dm, h);
+    rows_qlinear(m, &L->q, h, B, q);
+    rows_qlinear(m, &L->k, h, B, k);
+    rows_qlinear(m, &L->v, h, B, v);
+    const float* qsrc = q;
+    const float* ksrc = k;
+    if (D->qk_norm) {
+      orc_rmsnorm(q, L->q_norm, goff, D->eps, B * nq, hd, qn);
+      orc_rmsnorm(k, L->k_norm, goff, D->eps, B * nkv, hd, kn);
+      qsrc = qn;
+      ksrc = kn;
+    }
+    /* rope into the scratch the norm left free: q -> at (then copied), k -> h */
+    float* qr = at;
+    float* kr = h;
+    orc_rope(qsrc, B, nq, hd, positions, d->rope_cos[ti], d->rope_sin[ti], qr);
+    orc_rope(ksrc, B, nkv, hd, positions, d->rope_cos[ti], d->rope_sin[ti], kr);
+    for (int32_t b = 0; b < B; b++) {
+      if (slots[b] < 0) continue;
+      int64_t base = (int64_t)slots[b] * kvr;
+      for (int32_t e = 0; e < kvr; e++) {
+        if (d->kv_f16) {
+          ((uint16_t*)d->kslab[l])[base + e] = orc_f32_to_f16(kr[(int64_t)b * kvr + e]);
+          ((uint16_t*)d->vslab[l])[base + e] = orc_f32_to_f16(v[(int64_t)b * kvr + e]);
+        } else {
+          ((float*)d->kslab[l])[base + e] = kr[(int64_t)b * kvr + e];
+          ((float*)d->vslab[l])[base + e] = v[(int64_t)b * kvr + e];
+        }
+      }
+    }
+    memcpy(qn, qr, sizeof(float) * (size_t)B * qd);
+    (void)esz;
+    orc_attention(qn, d->kslab[l], d->vslab[l], d->kv_f16, d->page_size, nkv, hd, nq, B, page_table,
+                  d->pps, lengths, window, D->attn_scale, d->split, at);
+    rows_qlinear(m, &L->o, at, B, o);
+    const float* oo = o;
+    if (D->sandwich) {
+      orc_rmsnorm(o, L->post_attn_norm, goff, D->eps, B, dm, o2);
+      oo = o2;
+    }
+    for (int64_t i = 0; i < (int64_t)B * dm; i++) x[i] = x[i] + oo[i];   /* xmid */
+    orc_rmsnorm(x, L->ffn_pre_norm, goff, D->eps, B, dm, h);
+    rows_qlinear(m, &L->gate, h, B, g);
+    rows_qlinear(m, &L->up, h, B, u);
+    for (int64_t i = 0; i < (int64_t)B * ff; i++) {
+      float a = D->ffn_geglu ? orc_gelu_tanh(g[i]) : orc_silu(g[i]);
+      g[i] = a * u[i];
+    }
+    rows_qlinear(m, &L->down, g, B, o);
+    oo = o;
+    if (D->sandwich) {
+      orc_rmsnorm(o, L->ffn_post_norm, goff, D->eps, B, dm, o2);
+      oo = o2;
+    }
+    for (int64_t i = 0; i < (int64_t)B * dm; i++) x[i] = x[i] + oo[i];
+  }
+  orc_rmsnorm(x, m->final_norm, goff, D->eps, B, dm, h);
+  rows_qlinear(m, &m->head, h, B, d->logits);
+  orc_argmax_rows(d->logits, B, D->vocab, tokens_out);
+  for (int32_t b = 0; b < B; b++) orc_embed_row(m, tokens_out[b], d->r0 + (int64_t)b * dm);
+  free(x); free(h); free(q); free(k); free(v); free(qn); free(kn); free(at);
+  free(o); free(o2); free(g); free(u);
+  return 0;
+}

@@ -1,0 +1,106 @@
+// device_math.h -- exact-by-construction device numerics for the decode step.
+//
+// Every function here performs the same sequence of correctly rounded IEEE
+// operations as its CPU restatement, so results are bit-identical.  The whole
+// library is compiled with -ffp-contract=off; fused multiply-adds are written
+// explicitly with __builtin_fmaf.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rstr {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// 2^k for k in [-126, 127], built from the exponent field.
+__device__ __forceinline__ float pow2i(int k) { return __int_as_float((k + 127) << 23); }
+
+// exp(x): Cody-Waite reduction by ln2 (hi/lo split), degree-7 Taylor series of
+// e^r on |r| <= ln2/2, then scaling by 2^n in two exact steps (so results that
+// land in the subnormal range round once).  Own implementation of the textbook
+// method; the constants are ln2, log2(e) and 1/k! rounded to float.
+__device__ __forceinline__ float dexp(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e43p+6f) return __builtin_inff();
+  if (x < -0x1.9fe36ap+6f) return 0.0f;
+  float n = __builtin_rintf(x * 0x1.715476p+0f);
+  float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+  r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0x1.0p-1f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  int n1 = ni / 2;
+  int n2 = ni - n1;
+  return (p * pow2i(n1)) * pow2i(n2);
+}
+
+// GELU in its tanh form, tanh(u) = 1 - 2/(e^{2u}+1).
+__device__ __forceinline__ float dgelu(float g) {
+  float g3 = (g * g) * g;
+  float u = 0x1.988454p-1f * (g + 0x1.6e4e26p-5f * g3);
+  float e = dexp(u + u);
+  float t = 1.0f - 2.0f / (e + 1.0f);
+  return (0.5f * g) * (1.0f + t);
+}
+
+__device__ __forceinline__ float dsilu(float g) { return g / (1.0f + dexp(-g)); }
+
+// fp32 -> fp16 with round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float h2f_bits(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// ---- counter-based synthetic weights --------------------------------------
+#define RSTR_GOLDEN 0x9E3779B97F4A7C15ull
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + RSTR_GOLDEN;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__host__ __device__ __forceinline__ uint64_t tensor_key(uint64_t seed, int layer, int role) {
+  uint64_t tag = ((uint64_t)(uint32_t)(layer + 1) << 16) | (uint64_t)(uint32_t)role;
+  return splitmix64(splitmix64(seed) ^ tag);
+}
+// Irwin-Hall sum of twelve 16-bit uniforms: exact integer sum, exact double
+// centring, one double multiply-add, one rounding to float.
+__device__ __forceinline__ float synth_normal(uint64_t key, uint64_t index, double mean, double std) {
+  uint64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    uint64_t r = splitmix64(key + (3u * index + (uint64_t)j) * RSTR_GOLDEN);
+    s += (r & 0xFFFFu) + ((r >> 16) & 0xFFFFu) + ((r >> 32) & 0xFFFFu) + (r >> 48);
+  }
+  double v = ((double)s + 6.0) / 65536.0 - 6.0;
+  return (float)(mean + std * v);
+}
+
+// ---- wavefront reductions ----------------------------------------------------
+// xor butterfly: level m combines lanes i and i^m.  Because fp add commutes,
+// both lanes hold the same value and the result is the balanced pairwise tree
+// over lane order.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+}  // namespace rstr

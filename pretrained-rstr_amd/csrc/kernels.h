@@ -1,0 +1,96 @@
+// kernels.h -- host-side launch interface of the gfx950 decode-step kernels.
+//
+// Device data layouts (all chosen for 128-bit coalesced loads on CDNA4):
+//
+//  Quantised linear W[N][K] (N % 16 == 0, K % 128 == 0, nb = K/32 blocks):
+//   column tile ct = n/16, block group bq = b/4, k-group g = (k%32)/8,
+//   lane column nn = n%16, block-in-group bb = b%4.
+//   Q4 dword  [ct][bq][g][nn][bb]  holds the 8 nibbles of weights
+//             k = 32b + 8g + {0..7}; nibble i carries k_local = {0,2,4,6,1,3,5,7}[i].
+//   Q8 dwords [ct][bq][g][nn][bb][2]; byte i carries k_local = {0,2,1,3,4,6,5,7}[i].
+//   fp16 scales [ct][bq][nn][bb].
+//   (These permutations make the nibble/byte -> fp16 expansion a mask-or plus
+//   one packed fp16 add; the canonical row-major order is restored on export.)
+//
+//  Quantised activation X[M][K] for the MFMA A operand (Mpad = 16*ceil(M/16)):
+//   fp16 integer values [Mpad/16][nb][g][m%16][8], fp32 block scales [nb][Mpad].
+//
+//  KV pages per layer and slab: fp16 [page][page_size][n_kv][head_dim]
+//   (the routed-append ABI of doc/serving-architecture.md:178-190).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rstr {
+
+struct QTensor {       // one device-resident quantised matrix
+  void* w = nullptr;   // packed dwords
+  uint16_t* s = nullptr;
+  int n = 0, k = 0, bits = 4;
+};
+
+struct ActBuf {        // quantised activations in MFMA tile order
+  _Float16* q = nullptr;
+  float* s = nullptr;
+  int mpad = 0;
+};
+
+// weights
+hipError_t launch_gen_linear(hipStream_t st, const QTensor& t, int col_off, int n_rows, int k,
+                             uint64_t key, const float* src_f32);
+hipError_t launch_gen_f32(hipStream_t st, float* out, int64_t n, uint64_t key, double mean,
+                          double std, double scale);
+hipError_t launch_prescale(hipStream_t st, float* out, const float* in, int64_t n, double scale);
+
+// projections
+hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
+                        int ldy);
+
+// row kernels
+hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,
+                            int rows, int n, ActBuf& out);
+hipError_t launch_post_attn(hipStream_t st, const float* o, const float* x, float* xmid,
+                            const float* paln, const float* pfln, float goff, float eps, int rows,
+                            int n, ActBuf& out);
+hipError_t launch_post_ffn(hipStream_t st, const float* dn, const float* xmid, float* xout,
+                           const float* pffln, const float* gnext, float goff, float eps, int rows,
+                           int n, ActBuf& out);
+hipError_t launch_act_quant(hipStream_t st, const float* gu, int rows, int ff, int geglu,
+                            ActBuf& out);
+hipError_t launch_qkv_post(hipStream_t st, const float* yqkv, int rows, int n_q, int n_kv, int hd,
+                           const float* qn, const float* kn, float goff, float eps,
+                           const float* cos_t, const float* sin_t, const int32_t* positions,
+                           const int32_t* slots, float* qr, uint16_t* kpages, uint16_t* vpages);
+
+// attention
+struct AttnGeom {
+  int batch, n_q, n_kv, hd, page_size, pps, split, window;
+  float scale;
+};
+hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
+                            int32_t* lane_tab);
+hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
+                             const uint16_t* kpages, const uint16_t* vpages,
+                             const int32_t* page_table, const int32_t* lengths,
+                             const int32_t* lane_tab, float* part, int max_items);
+hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
+                             const int32_t* lane_tab, const float* part, float* out_f32,
+                             ActBuf* out_q);
+
+// tail, priming, pages
+hipError_t launch_argmax_gather(hipStream_t st, const float* logits, int rows, int vocab,
+                                const float* emb, int d, int32_t* tok, float* r0);
+hipError_t launch_gather_rows(hipStream_t st, const float* emb, int d, const int32_t* lanes,
+                              const int32_t* tokens, int n, float* r0);
+hipError_t launch_append_rows(hipStream_t st, const float* k_rows, const float* v_rows, int rows,
+                              int kvr, const int32_t* slots, uint16_t* kpages, uint16_t* vpages);
+hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64_t page_elems,
+                             const int32_t* pairs, int npairs);
+hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
+                                 int64_t page_elems, const int32_t* pages, int npages,
+                                 uint64_t seed);
+
+// lane table layout (int32): lo[B] k0[B] nsplit[B] base[B+1]
+inline int lane_tab_words(int batch) { return 4 * batch + 1; }
+
+}  // namespace rstr

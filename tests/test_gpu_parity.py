@@ -1,0 +1,386 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Integer/byte/index results (packed weights, page contents, token ids) must be
+bit-exact; this build also holds every float intermediate bit-exact (logits,
+resident rows, attention outputs) because the kernels follow the oracle's
+canonical operation order.  The reference's own device KATs are reproduced
+first (continuation_paged_attention_device_test.clj:42-174,
+continuation_paged_append_device_test.clj:30-119).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lanes import Routes
+from rstr import configs, hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sess():
+    s = hip.Session(0)
+    yield s
+    s.close()
+
+
+def _cfg(name, **kw):
+    c = dict(configs.MODELS[name])
+    c.update(kw)
+    return c
+
+
+# ---------------------------------------------------------------------------
+# weights
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name,bits", [("tiny_gemma", 4), ("tiny_llama", 4), ("tiny_qwen", 8),
+                                       ("tiny_llama", 8)])
+def test_synthetic_weights_bit_exact(sess, name, bits):
+    cfg = configs.with_bits(configs.MODELS[name], bits)
+    print(f"case weights {name} q{bits}", flush=True)
+    m = hip.Model(sess, cfg, seed=5)
+    om = O.Model(cfg, seed=5)
+    try:
+        for layer in range(cfg["n_layers"]):
+            for role in ("q", "k", "v", "o", "gate", "up", "down"):
+                gw, gs = m.export_linear(layer, role)
+                ow, osc = om.tensor(layer, role)
+                assert np.array_equal(gw, ow), (layer, role)
+                assert np.array_equal(gs, osc), (layer, role)
+        gw, gs = m.export_linear(-1, "embed")
+        ow, osc = om.tensor(-1, "embed")
+        assert np.array_equal(gw, ow) and np.array_equal(gs, osc)
+    finally:
+        m.close()
+
+
+def _edge_matrix(n, k, seed):
+    """Weights with the quantiser's edge cases: zero blocks, signed ties, tiny and
+    huge magnitudes, exact multiples of the step."""
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k)).astype(np.float32) * np.float32(0.02)
+    w[0, :32] = 0.0
+    w[1, :32] = 0.5
+    w[1, 5] = -0.5                     # |max| tie between signs: first occurrence wins
+    w[2, :32] = np.linspace(-8, 7, 32, dtype=np.float32)   # exact grid
+    w[3, :32] = 1e-30
+    w[4, :32] = 6e4
+    w[5, 32:64] = -rng.random(32).astype(np.float32)
+    return w
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_host_tensor_bind_quantises_like_the_oracle(sess, bits):
+    cfg = configs.with_bits(configs.TINY_LLAMA, bits)
+    print(f"case host-bind q{bits}", flush=True)
+    tensors = []
+    expect = {}
+    seed = 11
+    for layer in range(cfg["n_layers"]):
+        for role in ("q", "k", "v", "o", "gate", "up", "down"):
+            n, k = O.linear_shape(cfg, role)
+            w = _edge_matrix(n, k, seed)
+            seed += 1
+            tensors.append((layer, role, w))
+            expect[(layer, role)] = O.quant_q4(w) if bits == 4 else O.quant_q8(w)
+        for role in ("attn_norm", "ffn_pre_norm"):
+            tensors.append((layer, role, np.ones(cfg["d_model"], np.float32)))
+    emb = _edge_matrix(cfg["vocab"], cfg["d_model"], 99)
+    tensors.append((-1, "embed", emb))
+    tensors.append((-1, "final_norm", np.ones(cfg["d_model"], np.float32)))
+    expect[(-1, "embed")] = O.quant_q4(emb) if bits == 4 else O.quant_q8(emb)
+    m = hip.Model(sess, cfg, tensors=tensors)
+    try:
+        for (layer, role), (ew, es) in expect.items():
+            gw, gs = m.export_linear(layer, role)
+            assert np.array_equal(gw, ew), (layer, role)
+            assert np.array_equal(gs, es), (layer, role)
+    finally:
+        m.close()
+
+
+def test_host_bind_rejects_missing_tensor(sess):
+    cfg = configs.TINY_LLAMA
+    with pytest.raises(hip.RstrError, match="missing"):
+        hip.Model(sess, cfg, tensors=[(-1, "final_norm", np.ones(cfg["d_model"]))])
+
+
+# ---------------------------------------------------------------------------
+# reference KATs: append and attention
+# ---------------------------------------------------------------------------
+def _kat_pool(sess, page_size=4, pages=4):
+    cfg = configs.TINY_GEMMA      # n_kv 1, head_dim 64: the KAT's 2/4-wide rows embed in dims 0..3
+    m = hip.Model(sess, cfg, seed=1)
+    return m, hip.Pool(m, page_size, pages)
+
+
+def _row(vals, hd=64):
+    r = np.zeros(hd, np.float32)
+    r[:len(vals)] = vals
+    return r
+
+
+def test_reference_attention_kat(sess):
+    """continuation_paged_attention_device_test.clj:42-174: K=[[1,0],[0,1]],
+    V=[[10,20],[30,40]], q=[1,0], scale 1/sqrt(2) -> [16.6048 26.6048]; a
+    one-token lane gives [5 7]; window-left 0 gives [30 40] and [5 7]."""
+    print("case attention KAT", flush=True)
+    m, p = _kat_pool(sess)
+    try:
+        # route a: pages [0] tokens 0,1 ; route b: page [1] token 0
+        p.append(0, [_row([1, 0]), _row([0, 1]), _row([1, 1])],
+                 [_row([10, 20]), _row([30, 40]), _row([5, 7])], [0, 1, 4])
+        q = np.stack([_row([1, 0]), _row([1, 0])])[:, None, :]
+        pt = np.array([[0, -1], [1, -1]], np.int32)
+        lengths = np.array([2, 1], np.int32)
+        out = p.attention(0, q, pt, lengths, scale=1 / math.sqrt(2.0))
+        got = np.concatenate([out[0, 0, :2], out[1, 0, :2]])
+        assert np.all(np.abs(got - np.array([16.6048, 26.6048, 5.0, 7.0])) < 1e-4), got
+        assert np.all(out[:, :, 2:] == 0)
+        # several history tiles (split 4 > route) give the same value
+        out2 = p.attention(0, q, pt, lengths, scale=1 / math.sqrt(2.0), split=4)
+        assert np.array_equal(out, out2)
+        win = p.attention(0, q, pt, lengths, scale=1 / math.sqrt(2.0), window=1)
+        assert np.array_equal(np.concatenate([win[0, 0, :2], win[1, 0, :2]]),
+                              np.array([30.0, 40.0, 5.0, 7.0], np.float32))
+    finally:
+        p.close()
+        m.close()
+
+
+def test_reference_append_kat(sess):
+    """continuation_paged_append_device_test.clj:30-119: rows land in fp16
+    (round to nearest even) exactly at their slots, every other element keeps
+    the sentinel 42.0, and append -> attention over the fresh row returns the
+    value row exactly."""
+    print("case append KAT", flush=True)
+    m, p = _kat_pool(sess, page_size=4, pages=3)
+    try:
+        hd = 64
+        sentinel = np.float16(42.0).view(np.uint16)
+        for slab in (0, 1):
+            p.upload(slab, 0, 0, np.full(3 * 4 * hd, sentinel, np.uint16))
+        k_rows = [_row([1.1, -2.2, 3.3, -4.4]), _row([5.5, -6.6, 7.7, -8.8])]
+        v_rows = [_row([0.25, -0.5, 0.75, -1.0]), _row([1.25, -1.5, 1.75, -2.0])]
+        slots = [4, 3]
+        p.append(0, k_rows, v_rows, slots)
+        kk = p.download(0, 0).reshape(12, hd)
+        vv = p.download(1, 0).reshape(12, hd)
+        for slot in range(12):
+            if slot in slots:
+                lane = slots.index(slot)
+                assert np.array_equal(kk[slot], k_rows[lane].astype(np.float16).view(np.uint16))
+                assert np.array_equal(vv[slot], v_rows[lane].astype(np.float16).view(np.uint16))
+            else:
+                assert np.all(kk[slot] == sentinel) and np.all(vv[slot] == sentinel)
+        # append then attention over the one-row route at slot 8 (page 2)
+        p.append(0, [k_rows[0]], [v_rows[0]], [8])
+        out = p.attention(0, np.array([[_row([1, 0, 0, 0])]]), np.array([[2]], np.int32),
+                          np.array([1], np.int32))
+        assert np.array_equal(out[0, 0, :4], np.array([0.25, -0.5, 0.75, -1.0], np.float32))
+    finally:
+        p.close()
+        m.close()
+
+
+def test_append_rejects_duplicate_slots(sess):
+    m, p = _kat_pool(sess)
+    try:
+        with pytest.raises(hip.RstrError, match="distinct"):
+            p.append(0, [_row([1])] * 2, [_row([1])] * 2, [3, 3])
+    finally:
+        p.close()
+        m.close()
+
+
+# ---------------------------------------------------------------------------
+# attention vs the oracle on random ragged inputs
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (256, 4, 1), (64, 8, 2), (128, 16, 8)])
+@pytest.mark.parametrize("split,window", [(256, 0), (32, 0), (16, 24)])
+def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
+    print(f"case attention hd{hd} q{n_q} kv{n_kv} split{split} window{window}", flush=True)
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
+               head_dim=hd)
+    B, ps, pages, pps = 7, 16, 96, 16
+    rng = np.random.default_rng(hd + split + window)
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        lengths = np.array([1, 0, 17, 255, 256, 100, 233], np.int32)
+        perm = rng.permutation(pages).astype(np.int32)
+        pt = np.full((B, pps), -1, np.int32)
+        used = 0
+        for b in range(B):
+            n = -(-lengths[b] // ps)
+            pt[b, :n] = perm[used:used + n]
+            used += n
+        q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        got = p.attention(0, q, pt, lengths, window=window, scale=scale, split=split)
+        want = O.attention(q, kp, vp, pt, lengths, window, scale, split)
+        assert np.array_equal(got, want)
+        # float64 softmax restatement: the canonical order stays within fp32 rounding
+        for b in range(B):
+            L = lengths[b]
+            if L == 0:
+                assert np.all(got[b] == 0)
+                continue
+            lo = max(0, L - window) if window else 0
+            ks = np.stack([kp[pt[b, t // ps], t % ps] for t in range(lo, L)]).astype(np.float64)
+            vs = np.stack([vp[pt[b, t // ps], t % ps] for t in range(lo, L)]).astype(np.float64)
+            for h in range(n_q):
+                kvh = h // (n_q // n_kv)
+                s = ks[:, kvh] @ q[b, h].astype(np.float64) * scale
+                w = np.exp(s - s.max())
+                ref = (w / w.sum()) @ vs[:, kvh]
+                assert np.max(np.abs(ref - got[b, h])) < 2e-5 * (1 + np.max(np.abs(ref)))
+    finally:
+        p.close()
+        m.close()
+
+
+# ---------------------------------------------------------------------------
+# full decode steps
+# ---------------------------------------------------------------------------
+def _run_lanes(sess, cfg, B, prefix, schedule, graph=True, split=16, ps=16, pages=80, pps=10,
+               maxpos=160, seed=3, kv_seed=17, tokens=None):
+    """Drive GPU and oracle decoders through the same descriptors; return both
+    token histories plus the decoders for further checks."""
+    routes = Routes(B, ps, pages, pps, seed=seed)
+    m = hip.Model(sess, cfg, seed=seed)
+    p = hip.Pool(m, ps, pages)
+    d = hip.Decoder(m, p, B, pps, maxpos, split)
+    d.set_graph(graph)
+    om = O.Model(cfg, seed=seed)
+    od = O.Decoder(om, B, ps, pages, pps, maxpos, kv_f16=True, split=split)
+    for b, n in enumerate(prefix):
+        new = routes.prefix(b, n)
+        if new:
+            p.fill_synthetic(new, kv_seed)
+            for pg in new:
+                od.fill_synthetic(pg, kv_seed)
+    toks = tokens if tokens is not None else (np.arange(B) * 37 + 5) % cfg["vocab"]
+    d.prime_lanes(np.arange(B), toks)
+    od.prime_lanes(np.arange(B), toks)
+    hist_g, hist_o = [], []
+    for active in schedule:
+        desc = routes.step(active)
+        g = d.step_lanes(**desc)
+        o = od.step_lanes(**desc)
+        act = np.array(sorted(active))
+        assert np.array_equal(g[act], o[act]), (g, o)
+        gl, ol = d.logits(), od.logits()
+        assert np.array_equal(gl[act], ol[act])
+        hist_g.append(g)
+        hist_o.append(o)
+    return dict(m=m, p=p, d=d, om=om, od=od, routes=routes, g=hist_g, o=hist_o)
+
+
+def _close(r):
+    r["d"].close()
+    r["p"].close()
+    r["m"].close()
+    r["od"].close()
+    r["om"].close()
+
+
+@pytest.mark.parametrize("name", ["tiny_gemma", "tiny_llama", "tiny_qwen"])
+@pytest.mark.parametrize("graph", [True, False])
+def test_decode_steps_bit_exact(sess, name, graph):
+    print(f"case decode {name} graph={graph}", flush=True)
+    cfg = configs.MODELS[name]
+    B = 6
+    prefix = [0, 17, 40, 3, 0, 60]
+    sched = [[0, 1, 2, 3, 5], [0, 1, 2, 3, 5], [1, 2, 5], [0, 1, 2, 3, 4, 5]] + [list(range(6))] * 4
+    r = _run_lanes(sess, cfg, B, prefix, sched, graph=graph)
+    try:
+        # every resident row and every page of every layer matches bit for bit
+        assert np.array_equal(r["d"].rows(), r["od"].r0())
+        for layer in range(cfg["n_layers"]):
+            for slab in (0, 1):
+                assert np.array_equal(r["p"].pages(slab, layer).view(np.uint16),
+                                      r["od"].slab(slab, layer).view(np.uint16)), (layer, slab)
+    finally:
+        _close(r)
+
+
+def test_lane_results_do_not_depend_on_the_batch(sess):
+    """A lane decoded alone and inside a batch of ragged neighbours yields the same
+    tokens and logits (the canonical orders are per row)."""
+    print("case batch invariance", flush=True)
+    cfg = configs.TINY_LLAMA
+    sched = [[0, 1, 2, 3, 4, 5, 6, 7, 8]] * 5
+    big = _run_lanes(sess, cfg, 9, [33, 5, 0, 70, 12, 1, 2, 44, 9], sched, tokens=np.full(9, 77))
+    one = _run_lanes(sess, cfg, 1, [33], [[0]] * 5, tokens=np.array([77]))
+    try:
+        assert [h[0] for h in big["g"]] == [h[0] for h in one["g"]]
+    finally:
+        _close(big)
+        _close(one)
+
+
+@pytest.mark.parametrize("name,layers", [("llama3_8b", 1), ("gemma3_270m", 6), ("qwen3_06b", 1)])
+def test_config_shapes_first_layers(sess, name, layers):
+    """Full-width config shapes (vocabulary included) with the first layers only:
+    one step of ragged lanes matches the oracle bit for bit."""
+    print(f"case shape {name} layers={layers}", flush=True)
+    cfg = _cfg(name, n_layers=layers)
+    B = 4
+    r = _run_lanes(sess, cfg, B, [700, 0, 33, 1500], [[0, 2, 3], [0, 1, 2, 3]], split=256,
+                   ps=16, pages=200, pps=100, maxpos=1600)
+    _close(r)
+
+
+def test_step_rejects_bad_descriptors(sess):
+    cfg = configs.TINY_LLAMA
+    m = hip.Model(sess, cfg, seed=1)
+    p = hip.Pool(m, 16, 8)
+    d = hip.Decoder(m, p, 2, 4, 64, 16)
+    try:
+        rows = np.arange(3)
+        pt = np.array([[0, -1, -1, -1], [-1] * 4])
+        good = dict(slots=[0, -1], row_offsets=rows, positions=[0, 0], page_table=pt,
+                    lengths=[1, 0], start_positions=[0, 0])
+        d.step_lanes(**good)
+        bad = dict(good, slots=[5, -1])
+        with pytest.raises(hip.RstrError, match="last token"):
+            d.step_lanes(**bad)
+        bad = dict(good, lengths=[1, 0], slots=[0, 3])
+        with pytest.raises(hip.RstrError, match="inactive"):
+            d.step_lanes(**bad)
+        bad = dict(good, page_table=np.array([[9, -1, -1, -1], [-1] * 4]), slots=[144, -1])
+        with pytest.raises(hip.RstrError):
+            d.step_lanes(**bad)
+        bad = dict(good, positions=[3, 0])
+        with pytest.raises(hip.RstrError, match="position"):
+            d.step_lanes(**bad)
+    finally:
+        d.close()
+        p.close()
+        m.close()
+
+
+def test_copy_page_copies_every_layer_and_slab(sess):
+    cfg = configs.TINY_GEMMA
+    m = hip.Model(sess, cfg, seed=1)
+    p = hip.Pool(m, 16, 6)
+    try:
+        p.fill_synthetic([2], seed=5)
+        p.copy_page(2, 4)
+        for layer in range(cfg["n_layers"]):
+            for slab in (0, 1):
+                a = p.pages(slab, layer)
+                assert np.array_equal(a[2].view(np.uint16), a[4].view(np.uint16))
+                assert np.any(a[2] != 0)
+    finally:
+        p.close()
+        m.close()
