@@ -1,0 +1,188 @@
+#!/usr/bin/env python3
+"""Benchmark: aggregate decode tokens/s of the resident continuous decode step on one
+MI355X, with the HBM roofline of the dominant kernel and the CPU oracle timed beside it.
+
+Default workload (the north-star target): Llama-3-8B-shaped
+decoder, Q4 block-32 weights, 128 continuous decode lanes with churn -- Poisson(4)
+arrivals per step, prompts U[128,4096], outputs U[32,512] -- admitted onto a fixed fp16
+page pool sized to 80% of free HBM.  Admitted prompts get synthetic fp16 K/V in their
+reserved pages (standing in for a restored prefix).  The host control plane plans every
+step up front; the timed region replays the device-resident schedule (fills, primes,
+descriptor copies, one step graph per step) and is bracketed by a device sync.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pretrained-rstr_amd"))
+
+from rstr import configs, hip, workload  # noqa: E402
+
+METRIC = "aggregate decode tokens/sec at N lanes; % of HBM roofline (GB/s) on 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
+    "config5": ("llama3_8b", 128, 16, 4096 + 512, (128, 4096), (32, 512), 4.0, 5),
+    "config2": ("gemma3_270m", 16, 16, 2048 + 256 + 1, (64, 2048), (256, 256), 0.0, 1),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg: dict, prefix: int, budget_s: float) -> dict:
+    """The reference CPU path restated in C (oracle): Q4 int8-MAC linears, f32 KV, one
+    lane at a time (decoder.clj:443-458 generate-cached), greedy; timed on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker / CPU baseline only
+    t0 = time.perf_counter()
+    model = O.Model(cfg, seed=1)
+    build_s = time.perf_counter() - t0
+    ps = 16
+    pps = -(-(prefix + 256) // ps)
+    dec = O.Decoder(model, 1, ps, pps, pps, prefix + 256, kv_f16=False, split=256)
+    for pg in range(-(-prefix // ps)):
+        dec.fill_synthetic(pg, 7)
+    dec.prime_lanes([0], [1])
+    steps, t1 = 0, time.perf_counter()
+    length = prefix
+    while True:
+        length += 1
+        t = length - 1
+        desc = dict(slots=[(t // ps) * ps + t % ps], row_offsets=[0, 1], positions=[t],
+                    page_table=[list(range(pps))], lengths=[length], start_positions=[0])
+        dec.step_lanes(**desc)
+        steps += 1
+        el = time.perf_counter() - t1
+        if el > budget_s or length >= prefix + 255:
+            break
+    threads = int(O.lib().orc_num_threads())
+    dec.close()
+    model.close()
+    return {"value": round(steps / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 lane, {prefix}-token synthetic prefix, {steps} greedy decode steps "
+                      f"({el:.1f} s; oracle model build {build_s:.1f} s untimed)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS))
+    ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--pool-fraction", type=float, default=0.8)
+    ap.add_argument("--split", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (the decode step "
+                                   "shards as independent replicas, see DESIGN.md)"}))
+        sys.exit(2)
+
+    name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
+    cfg = configs.MODELS[name]
+    pps = -(-maxpos // ps)
+    sess = hip.Session(0)
+    t0 = time.perf_counter()
+    model = hip.Model(sess, cfg, seed=1)
+    log(f"model bound in {time.perf_counter() - t0:.1f}s, weights {model.weight_bytes / 1e9:.2f} GB")
+    free, total = sess.memory()
+    page_bytes = 2 * cfg["n_layers"] * ps * cfg["n_kv"] * cfg["head_dim"] * 2
+    reserve = 8 << 30  # decoder scratch, templates, schedule
+    physical = int(args.pool_fraction * (free - reserve) // page_bytes)
+    t0 = time.perf_counter()
+    pool = hip.Pool(model, ps, physical)
+    log(f"page pool: {physical} pages x {page_bytes >> 20} MiB = {physical * page_bytes / 1e9:.1f} GB "
+        f"({time.perf_counter() - t0:.1f}s)")
+    dec = hip.Decoder(model, pool, lanes, pps, maxpos, args.split)
+
+    # ---- plan the whole run on the host (control-plane mirror) -------------------------
+    n_total = args.warmup + args.steps + args.profile_steps
+    planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed, arrival_mean=arrivals,
+                                    prompt=prompt, output=output)
+    t0 = time.perf_counter()
+    plan = [planner.plan_step() for _ in range(n_total)]
+    plan_s = time.perf_counter() - t0
+    host_ms_step = 1e3 * planner.host_seconds / n_total
+    log(f"planned {n_total} steps in {plan_s:.1f}s ({host_ms_step:.2f} ms/step host bookkeeping), "
+        f"retired {planner.retired}, rejected admissions {planner.rejected_admissions}")
+    t0 = time.perf_counter()
+    dec.schedule_upload(plan)
+    log(f"schedule uploaded in {time.perf_counter() - t0:.1f}s")
+
+    # ---- warmup, then the timed region ---------------------------------------------
+    _, warm_ms = dec.schedule_run(0, args.warmup)
+    log(f"warmup {args.warmup} steps: {warm_ms:.1f} ms (includes initial prefix fills)")
+    toks, dev_ms = dec.schedule_run(args.warmup, args.steps)
+    timed = plan[args.warmup:args.warmup + args.steps]
+    tokens = sum(st["active"] for st in timed)
+    ms_per_step = dev_ms / args.steps
+    value = tokens / (dev_ms / 1e3)
+    bytes_steps = [workload.step_bytes(cfg, st, model.weight_bytes) for st in timed]
+    step_bytes = float(np.mean([b["total"] for b in bytes_steps]))
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"timed {args.steps} steps: {dev_ms:.1f} ms, {ms_per_step:.3f} ms/step, {value:.0f} tok/s, "
+        f"{step_bytes / 1e9:.2f} GB/step algorithmic -> {step_gbs:.0f} GB/s")
+
+    # ---- per-kernel profile pass (eager, HIP events around each launch) -------------
+    first = args.warmup + args.steps
+    prof = dec.profile_steps(first, args.profile_steps)
+    prof_plan = plan[first:first + args.profile_steps]
+    attn_bytes = np.mean([np.mean(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in prof_plan])
+    attn_ms, attn_n = prof["attn_split"]
+    attn_avg_ms = attn_ms / max(attn_n, 1)
+    attn_gbs = attn_bytes / (attn_avg_ms * 1e-3) / 1e9
+    qg_ms, qg_n = prof["qgemm"]
+    log("profile (ms total / launches): " + ", ".join(f"{k} {v[0]:.2f}/{v[1]}" for k, v in prof.items()))
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"attn_split_{args.workload}_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4/int8 block dots exact, fp32 accumulate, fp16 KV",
+        "data": "synthetic (seeded random-init weights, synthetic prefix K/V, Poisson churn)",
+        "config": {"workload": f"{args.workload}: {name}-shaped Q4 decoder, {lanes} continuous lanes, "
+                               f"prompts U{list(prompt)}, outputs U{list(output)}, "
+                               f"Poisson({arrivals}) arrivals/step",
+                   "lanes": lanes, "page_size": ps, "physical_pages": physical,
+                   "attention_split": args.split, "parallelism": "1 GPU (replica)"},
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_attn_split (paged attention, per layer launch)",
+                     "bytes_per_launch": int(attn_bytes), "avg_launch_ms": round(attn_avg_ms, 4)},
+        "step_roofline": {"bytes_per_step": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "kernel_ms_per_step": {k: round(v[0] / args.profile_steps, 3) for k, v in prof.items()},
+        "host_bookkeeping_ms_per_step": round(host_ms_step, 3),
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(cfg, prefix=int(np.mean(prompt)), budget_s=args.cpu_seconds)
+        except Exception as e:  # the baseline must not hide the GPU number
+            out["cpu_baseline"] = {"error": repr(e)}
+    dec.close()
+    pool.close()
+    model.close()
+    sess.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

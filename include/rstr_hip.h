@@ -76,6 +76,8 @@ int rstr_session_close(rstr_session* s);
 const char* rstr_last_error(const rstr_session* s);
 /* Message of the last failure of an open call that returned no session. */
 const char* rstr_open_error(void);
+/* Free and total device memory of the session's GPU (pool sizing). */
+int rstr_session_memory(rstr_session* s, int64_t* free_bytes, int64_t* total_bytes);
 
 /* ---- model binding ----------------------------------------------------------
  * Replaces bind-decode! quantise + alloc + resident specs
@@ -185,6 +187,9 @@ typedef struct rstr_staged_step {
   uint64_t fill_seed;
   const int32_t* cow_pairs;   /* (src, dst) page copies before the step */
   int32_t n_cow;
+  const int32_t* prime_lanes; /* lanes primed with token embeddings before the step */
+  const int32_t* prime_tokens;
+  int32_t n_prime;
 } rstr_staged_step;
 int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* steps, int32_t n_steps);
 /* Runs staged steps [first, first+count); tokens_out[count][batch]; device_ms

@@ -89,6 +89,7 @@ def lib():
             "orc_fill_synthetic": (None, [P, i32, u64]),
             "orc_slab": (P, [P, i32, i32]),
             "orc_last_error": (C.c_char_p, []),
+            "orc_num_threads": (C.c_int, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -231,7 +232,10 @@ class Model:
             self.h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def tensor(self, layer: int, role: str):
         cfg = self.cfg
@@ -285,7 +289,10 @@ class Decoder:
             self.h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def prime_lanes(self, lanes, tokens):
         lanes, tokens = i32(lanes), i32(tokens)

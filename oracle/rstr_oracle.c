@@ -15,7 +15,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <omp.h>
+
 static __thread char g_err[256];
+int orc_num_threads(void) { return omp_get_max_threads(); }
 static void set_err(const char* msg) { snprintf(g_err, sizeof g_err, "%s", msg); }
 const char* orc_last_error(void) { return g_err; }
 
@@ -757,21 +760,26 @@ void orc_copy_page(orc_decoder* d, int32_t src, int32_t dst) {
   }
 }
 
-/* Synthetic N(0,1) K/V for one physical page in every layer: the stand-in  */
-/* for a restored prefix used by the throughput configurations.             */
+/* Synthetic K/V for one physical page in every layer: the stand-in for a   */
+/* restored prefix.  Page p copies template t = (splitmix64(seed^p)>>32) % 64 */
+/* of (layer, slab), whose element e is N(0,1) keyed by (seed, layer,        */
+/* 64+slab) at index t*page_elems + e.                                       */
+#define ORC_SYNTH_TEMPLATES 64
 void orc_fill_synthetic(orc_decoder* d, int32_t page, uint64_t seed) {
   int64_t pe = (int64_t)d->page_size * d->m->d.n_kv * d->m->d.head_dim;
+  uint64_t t = (orc_splitmix64(seed ^ (uint64_t)(int64_t)page) >> 32) % ORC_SYNTH_TEMPLATES;
   for (int32_t l = 0; l < d->m->d.n_layers; l++) {
     for (int s = 0; s < 2; s++) {
       uint64_t key = orc_tensor_key(seed, l, 64 + s);
       void* slab = s == 0 ? d->kslab[l] : d->vslab[l];
+#pragma omp parallel for schedule(static)
       for (int64_t e = 0; e < pe; e++) {
-        uint64_t idx = (uint64_t)page * (uint64_t)pe + (uint64_t)e;
-        float v = orc_normal(key, idx, 0.0, 1.0);
+        float v = orc_normal(key, t * (uint64_t)pe + (uint64_t)e, 0.0, 1.0);
+        int64_t idx = (int64_t)page * pe + e;
         if (d->kv_f16)
           ((uint16_t*)slab)[idx] = orc_f32_to_f16(v);
         else
-          ((float*)slab)[idx] = v;
+          ((float*)slab)[idx] = orc_f16_to_f32(orc_f32_to_f16(v));
       }
     }
   }

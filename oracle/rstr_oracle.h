@@ -116,6 +116,7 @@ void orc_fill_synthetic(orc_decoder* d, int32_t page, uint64_t seed);
 /* Raw page-slab access: slab 0 = key, 1 = value.  Element type is fp16 bits or f32. */
 void* orc_slab(orc_decoder* d, int32_t slab, int32_t layer);
 const char* orc_last_error(void);
+int orc_num_threads(void);
 
 #ifdef __cplusplus
 }

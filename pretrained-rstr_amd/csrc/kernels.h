@@ -42,22 +42,30 @@ hipError_t launch_gen_f32(hipStream_t st, float* out, int64_t n, uint64_t key, d
                           double std, double scale);
 hipError_t launch_prescale(hipStream_t st, float* out, const float* in, int64_t n, double scale);
 
-// projections
+// projections.  A projection whose K range is split over S workgroups writes S
+// output slices `stride` floats apart; consumers combine them in the canonical
+// tree order, (s0+s1) or ((s0+s1)+(s2+s3)).
+struct Slices {
+  const float* p;
+  int n;
+  size_t stride;
+};
+int qgemm_splits(int n, int mpad);
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
-                        int ldy);
+                        int ldy, int splits, size_t slice_stride);
 
 // row kernels
 hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,
                             int rows, int n, ActBuf& out);
-hipError_t launch_post_attn(hipStream_t st, const float* o, const float* x, float* xmid,
+hipError_t launch_post_attn(hipStream_t st, Slices o, const float* x, float* xmid,
                             const float* paln, const float* pfln, float goff, float eps, int rows,
                             int n, ActBuf& out);
-hipError_t launch_post_ffn(hipStream_t st, const float* dn, const float* xmid, float* xout,
+hipError_t launch_post_ffn(hipStream_t st, Slices dn, const float* xmid, float* xout,
                            const float* pffln, const float* gnext, float goff, float eps, int rows,
                            int n, ActBuf& out);
-hipError_t launch_act_quant(hipStream_t st, const float* gu, int rows, int ff, int geglu,
+hipError_t launch_act_quant(hipStream_t st, Slices gu, int rows, int ff, int geglu,
                             ActBuf& out);
-hipError_t launch_qkv_post(hipStream_t st, const float* yqkv, int rows, int n_q, int n_kv, int hd,
+hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n_kv, int hd,
                            const float* qn, const float* kn, float goff, float eps,
                            const float* cos_t, const float* sin_t, const int32_t* positions,
                            const int32_t* slots, float* qr, uint16_t* kpages, uint16_t* vpages);
@@ -86,9 +94,12 @@ hipError_t launch_append_rows(hipStream_t st, const float* k_rows, const float* 
                               int kvr, const int32_t* slots, uint16_t* kpages, uint16_t* vpages);
 hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64_t page_elems,
                              const int32_t* pairs, int npairs);
+#define RSTR_SYNTH_TEMPLATES 64
+hipError_t launch_gen_templates(hipStream_t st, uint16_t* tmpl, int n_layers, int64_t page_elems,
+                                uint64_t seed);
 hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
-                                 int64_t page_elems, const int32_t* pages, int npages,
-                                 uint64_t seed);
+                                 int64_t page_elems, const uint16_t* tmpl, const int32_t* pages,
+                                 int npages, uint64_t seed);
 
 // lane table layout (int32): lo[B] k0[B] nsplit[B] base[B+1]
 inline int lane_tab_words(int batch) { return 4 * batch + 1; }

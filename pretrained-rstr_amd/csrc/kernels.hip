@@ -168,139 +168,257 @@ __device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1) {
   return r;
 }
 
-struct GemmCtx {
-  const uint32_t* Wt;
-  const uint16_t* St;
-  const _Float16* X;
-  const float* Xs;
-  int nb, mpad, mt, rt0, c, nn, g, wave;
-};
-
-template <int RT, int BITS>
-__device__ __forceinline__ void part_sum(const GemmCtx& cx, int part, float (&acc)[RT][4]) {
+// Workgroup: 4 waves.  With RH row halves the waves form CTW = 4/RH column
+// tiles (16 columns each) x RH groups of RT row tiles.  Each wave owns its
+// output tile over the workgroup's whole K range (64/S contiguous parts, a
+// complete subtree of the canonical tree), so it accumulates parts in order and
+// merges leaves with a binary-counter stack.  Activations are staged through a
+// double-buffered LDS ring in chunks of 4 blocks and shared by all waves;
+// weights stream as one 128-bit load per lane per chunk.  With S > 1 the K
+// subtrees land in S output slices that the consumer combines as
+// (s0+s1) or ((s0+s1)+(s2+s3)).
+// Merge leaf `v` into the stack: t1 = trailing ones of the leaf index is the
+// number of completed left siblings.  Written as compile-time recursion so every
+// stack index is a constant before register promotion.
+template <int T, int RT, int LOGP>
+__device__ __forceinline__ void push_rec(int t1, float (&st)[LOGP][RT][4], float (&v)[RT][4],
+                                         float (&fin)[RT][4]) {
+  if constexpr (T == LOGP) {
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++)
+    for (int i = 0; i < RT; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) acc[rt][r] = 0.0f;
-  int b0 = part * cx.c;
-  int b1 = min(cx.nb, b0 + cx.c);
-  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int b = b0; b < b1; ++b) {
-    int bq = b >> 2, bb = b & 3;
-    size_t widx = (((size_t)bq * 4 + cx.g) * 16 + cx.nn) * 4 + bb;
-    h8 wv;
-    if (BITS == 4) {
-      wv = unpack_q4(cx.Wt[widx]);
+      for (int r = 0; r < 4; r++) fin[i][r] = v[i][r];
+  } else {
+    if (t1 == T) {
+#pragma unroll
+      for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) st[T][i][r] = v[i][r];
     } else {
-      const uint2 q = reinterpret_cast<const uint2*>(cx.Wt)[widx];
-      wv = unpack_q8(q.x, q.y);
-    }
-    float dw = h2f_bits(cx.St[((size_t)bq * 16 + cx.nn) * 4 + bb]);
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      int rtile = cx.rt0 + rt;
-      if (rtile < cx.mt) {
-        const h8 av = *reinterpret_cast<const h8*>(
-            cx.X + ((((size_t)rtile * cx.nb + b) * 4 + cx.g) * 16 + cx.nn) * 8);
-        f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, wv, zero, 0, 0, 0);
-        const f4 xs = *reinterpret_cast<const f4*>(cx.Xs + (size_t)b * cx.mpad + rtile * 16 + cx.g * 4);
+      for (int i = 0; i < RT; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[rt][r] = __builtin_fmaf(d[r], dw * xs[r], acc[rt][r]);
-      }
+        for (int r = 0; r < 4; r++) v[i][r] = st[T][i][r] + v[i][r];
+      push_rec<T + 1, RT, LOGP>(t1, st, v, fin);
     }
   }
 }
 
-// Push leaf P of a 16-leaf pairwise tree: merge completed left siblings.
-template <int P, int RT>
-__device__ __forceinline__ void push_leaf(float (&st)[4][RT][4], const float (&acc)[RT][4],
-                                          float (&fin)[RT][4]) {
-  constexpr int T = ((P & 1) == 0) ? 0 : ((P & 3) != 3) ? 1 : ((P & 7) != 7) ? 2 : ((P & 15) != 15) ? 3 : 4;
+template <int RT, int LOGP>
+__device__ __forceinline__ void push_leaf_dyn(int leaf, float (&st)[LOGP][RT][4], float (&v)[RT][4],
+                                              float (&fin)[RT][4]) {
+  push_rec<0, RT, LOGP>(__builtin_ctz(~(unsigned)leaf), st, v, fin);
+}
+
+constexpr int QG_MT = 8;   // row tiles staged per workgroup (128 rows)
+
+template <int RT, int RH, int BITS, int LOGP>
+__global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W,
+                                                  const uint16_t* __restrict__ Ws,
+                                                  const _Float16* __restrict__ X,
+                                                  const float* __restrict__ Xs, int nb, int mpad,
+                                                  float* __restrict__ Y, int ldy, int m_rows,
+                                                  size_t slice_stride) {
+  constexpr int CTW = 4 / RH;
+  constexpr int DW = BITS == 4 ? 1 : 2;
+  constexpr int PPW = 1 << LOGP;
+  __shared__ u32x4 s_act[2][QG_MT * 4 * 64];     // [buf][rt][bb][64 x 16B]
+  __shared__ float s_xs[2][4][QG_MT * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nn = lane & 15, g = lane >> 4;
+  const int ctw = wave % CTW, rh = wave / CTW;
+  const int ct = blockIdx.x * CTW + ctw;
+  const int q = blockIdx.y;
+  const int rg = blockIdx.z;                       // group of QG_MT row tiles
+  const int mt_all = mpad >> 4;
+  const int mt = min(QG_MT, mt_all - rg * QG_MT);  // row tiles in this group
+  const int nb4 = nb >> 2;
+  const int c = (nb + 63) >> 6;
+  const int p0 = q * PPW;
+  const int b_begin = min(nb, p0 * c), b_end = min(nb, (p0 + PPW) * c);
+  const int nchunk = (b_end - b_begin) >> 2;
+  const uint32_t* Wt = W + (size_t)ct * nb4 * 256 * DW;
+  const uint16_t* St = Ws + (size_t)ct * nb4 * 64;
+  const u32x4* Xg = reinterpret_cast<const u32x4*>(X) + (size_t)rg * QG_MT * nb * 64;
+  const int pieces = mt * 256;                     // 16-byte act pieces per chunk
+  const int row0 = rg * QG_MT * 16;
+
+  float st[LOGP][RT][4];
+  float acc[RT][4], fin[RT][4];
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++)
+  for (int i = 0; i < RT; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) { acc[i][r] = 0.0f; fin[i][r] = 0.0f; }
+
+  // register staging for the next chunk (macros, so every array index is a
+  // compile-time constant and stays in registers)
+  u32x4 pa[QG_MT];
+  float pxs[2];
+  u32x4 pw[DW];
+  u32x2 psc;
+#define QG_LOAD_CHUNK(CH)                                                                        \
+  do {                                                                                           \
+    const int b0_ = b_begin + 4 * (CH), bq_ = b0_ >> 2;                                          \
+    _Pragma("unroll") for (int k = 0; k < QG_MT; k++) {                                          \
+      const int piece = min(tid + 256 * k, pieces - 1);                                          \
+      pa[k] = Xg[((size_t)(piece >> 8) * nb + b0_) * 64 + (piece & 255)];                         \
+    }                                                                                            \
+    _Pragma("unroll") for (int k = 0; k < 2; k++) {                                              \
+      const int e = tid + 256 * k;                                                               \
+      const int rr = e & 127;                                                                    \
+      const float v_ = Xs[(size_t)(b0_ + (e >> 7)) * mpad + row0 + min(rr, mt * 16 - 1)];         \
+      pxs[k] = (rr < mt * 16) ? v_ : 0.0f;                                                       \
+    }                                                                                            \
+    const u32x4* wp_ = reinterpret_cast<const u32x4*>(Wt + ((size_t)bq_ * 256 + (g * 16 + nn) * 4) * DW); \
+    _Pragma("unroll") for (int k = 0; k < DW; k++) pw[k] = wp_[k];                               \
+    psc = *reinterpret_cast<const u32x2*>(St + ((size_t)bq_ * 16 + nn) * 4);                     \
+  } while (0)
+#define QG_STORE_CHUNK(BUF)                                                                      \
+  do {                                                                                           \
+    _Pragma("unroll") for (int k = 0; k < QG_MT; k++) s_act[(BUF)][tid + 256 * k] = pa[k];       \
+    _Pragma("unroll") for (int k = 0; k < 2; k++) {                                              \
+      const int e = tid + 256 * k;                                                               \
+      s_xs[(BUF)][e >> 7][e & 127] = pxs[k];                                                     \
+    }                                                                                            \
+  } while (0)
+
+  int leaf = 0;  // next leaf (part) index relative to p0
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (nchunk > 0) {
+    QG_LOAD_CHUNK(0);
+    QG_STORE_CHUNK(0);
+  }
+  __syncthreads();
+  for (int ch = 0; ch < nchunk; ch++) {
+    const int buf = ch & 1;
+    u32x4 cw[DW];
+#pragma unroll
+    for (int k = 0; k < DW; k++) cw[k] = pw[k];
+    const u32x2 csc = psc;
+    if (ch + 1 < nchunk) QG_LOAD_CHUNK(ch + 1);
+    const int b0 = b_begin + 4 * ch;
+#pragma unroll
+    for (int bb = 0; bb < 4; bb++) {
+      h8 wv;
+      if (BITS == 4) {
+        const uint32_t x = bb == 0 ? cw[0][0] : bb == 1 ? cw[0][1] : bb == 2 ? cw[0][2] : cw[0][3];
+        wv = unpack_q4(x);
+      } else {
+        const u32x4 lo = cw[bb >> 1];
+        const uint32_t x0 = (bb & 1) ? lo[2] : lo[0], x1 = (bb & 1) ? lo[3] : lo[1];
+        wv = unpack_q8(x0, x1);
+      }
+      const uint32_t sh = (bb < 2) ? csc[0] : csc[1];
+      const float dw = h2f_bits((uint16_t)((bb & 1) ? (sh >> 16) : (sh & 0xFFFFu)));
+#pragma unroll
+      for (int i = 0; i < RT; i++) {
+        const int rt = rh * RT + i;
+        if (rt < mt) {
+          const u32x4 a4 = s_act[buf][(rt * 4 + bb) * 64 + g * 16 + nn];
+          const h8 av = __builtin_bit_cast(h8, a4);
+          const f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, wv, zero, 0, 0, 0);
+          const f4 xs = *reinterpret_cast<const f4*>(&s_xs[buf][bb][rt * 16 + g * 4]);
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][r] = __builtin_fmaf(d[r], dw * xs[r], acc[i][r]);
+        }
+      }
+      const int b = b0 + bb;
+      if ((b + 1) % c == 0 || b + 1 == nb) {
+        push_leaf_dyn<RT, LOGP>(leaf, st, acc, fin);
+        leaf++;
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][r] = 0.0f;
+      }
+    }
+    if (ch + 1 < nchunk) QG_STORE_CHUNK(buf ^ 1);
+    __syncthreads();
+  }
+#undef QG_LOAD_CHUNK
+#undef QG_STORE_CHUNK
+  // empty trailing parts of the subtree
+  for (; leaf < PPW; leaf++) {
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][r] = 0.0f;
+    push_leaf_dyn<RT, LOGP>(leaf, st, acc, fin);
+  }
+  float* Yq = Y + (size_t)q * slice_stride;
+  const int col = ct * 16 + nn;
+#pragma unroll
+  for (int i = 0; i < RT; i++) {
+    const int rt = rh * RT + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      float v = acc[rt][r];
-      if constexpr (T >= 1) v = st[0][rt][r] + v;
-      if constexpr (T >= 2) v = st[1][rt][r] + v;
-      if constexpr (T >= 3) v = st[2][rt][r] + v;
-      if constexpr (T >= 4) v = st[3][rt][r] + v;
-      if constexpr (T == 4) fin[rt][r] = v;
-      else st[T][rt][r] = v;
+      const int m = row0 + rt * 16 + g * 4 + r;
+      if (rt < mt && m < m_rows) Yq[(size_t)m * ldy + col] = fin[i][r];
     }
-}
-
-template <int RT, int BITS, int P = 0>
-__device__ __forceinline__ void run_parts(const GemmCtx& cx, float (&st)[4][RT][4], float (&fin)[RT][4]) {
-  if constexpr (P < 16) {
-    float acc[RT][4];
-    part_sum<RT, BITS>(cx, cx.wave * 16 + P, acc);
-    push_leaf<P, RT>(st, acc, fin);
-    run_parts<RT, BITS, P + 1>(cx, st, fin);
   }
 }
 
-template <int RT, int BITS>
-__global__ __launch_bounds__(256) void k_qgemm(const uint32_t* __restrict__ W,
-                                               const uint16_t* __restrict__ Ws,
-                                               const _Float16* __restrict__ X,
-                                               const float* __restrict__ Xs, int nb, int mpad,
-                                               float* __restrict__ Y, int ldy, int m_rows) {
-  __shared__ float red[4][RT * 4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  constexpr int DW = BITS == 4 ? 1 : 2;
-  GemmCtx cx;
-  cx.nb = nb;
-  cx.mpad = mpad;
-  cx.mt = mpad >> 4;
-  cx.rt0 = blockIdx.y * RT;
-  cx.c = (nb + 63) >> 6;
-  cx.nn = lane & 15;
-  cx.g = lane >> 4;
-  cx.wave = wave;
-  cx.Wt = W + (size_t)blockIdx.x * (nb >> 2) * 256 * DW;
-  cx.St = Ws + (size_t)blockIdx.x * (nb >> 2) * 64;
-  cx.X = X;
-  cx.Xs = Xs;
-  float st[4][RT][4];
-  float fin[RT][4];
-  run_parts<RT, BITS>(cx, st, fin);
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) red[wave][rt * 4 + r][lane] = fin[rt][r];
-  __syncthreads();
-  if (wave == 0) {
-    int col = blockIdx.x * 16 + cx.nn;
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        int i = rt * 4 + r;
-        float v = (red[0][i][lane] + red[1][i][lane]) + (red[2][i][lane] + red[3][i][lane]);
-        int m = (cx.rt0 + rt) * 16 + cx.g * 4 + r;
-        if (m < m_rows) Y[(size_t)m * ldy + col] = v;
-      }
-  }
+int qgemm_splits(int n, int mpad) {
+  const int mt = mpad / 16;
+  const int rh = mt > 4 ? 2 : 1;
+  const int ctw = 4 / rh;
+  const int wgs = (n / 16 + ctw - 1) / ctw * ((mt + QG_MT - 1) / QG_MT);
+  if (wgs >= 512) return 1;
+  if (wgs * 2 >= 512) return 2;
+  return 4;
 }
 
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
-                        int ldy) {
-  int nb = w.k / 32;
-  int mt = x.mpad / 16;
-  int rt = mt >= 4 ? 4 : (mt >= 2 ? 2 : 1);
-  dim3 grid(w.n / 16, (mt + rt - 1) / rt);
+                        int ldy, int splits, size_t slice_stride) {
+  const int nb = w.k / 32;
+  const int mt_all = x.mpad / 16;
+  const int mt = mt_all < QG_MT ? mt_all : QG_MT;
+  const int rh = mt > 4 ? 2 : 1;
+  const int rt = rh == 2 ? 4 : (mt > 2 ? 4 : (mt > 1 ? 2 : 1));
+  const int ctw = 4 / rh;
+  if ((w.n / 16) % ctw) return hipErrorInvalidValue;
+  dim3 grid(w.n / 16 / ctw, splits, (mt_all + QG_MT - 1) / QG_MT);
   const uint32_t* W = (const uint32_t*)w.w;
-#define RSTR_QG(R, B)                                                                          \
-  hipLaunchKernelGGL((k_qgemm<R, B>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
-                     ldy, m_rows)
-  if (w.bits == 4) {
-    if (rt == 4) RSTR_QG(4, 4); else if (rt == 2) RSTR_QG(2, 4); else RSTR_QG(1, 4);
-  } else {
-    if (rt == 4) RSTR_QG(4, 8); else if (rt == 2) RSTR_QG(2, 8); else RSTR_QG(1, 8);
-  }
+#define RSTR_QG(R, H, B, LP)                                                                       \
+  hipLaunchKernelGGL((k_qgemm<R, H, B, LP>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
+                     ldy, m_rows, slice_stride)
+#define RSTR_QG_S(R, H, B)                                 \
+  do {                                                     \
+    if (splits == 1) RSTR_QG(R, H, B, 6);                  \
+    else if (splits == 2) RSTR_QG(R, H, B, 5);             \
+    else RSTR_QG(R, H, B, 4);                              \
+  } while (0)
+#define RSTR_QG_R(B)                                       \
+  do {                                                     \
+    if (rh == 2) RSTR_QG_S(4, 2, B);                       \
+    else if (rt == 4) RSTR_QG_S(4, 1, B);                  \
+    else if (rt == 2) RSTR_QG_S(2, 1, B);                  \
+    else RSTR_QG_S(1, 1, B);                               \
+  } while (0)
+  if (splits != 1 && splits != 2 && splits != 4) return hipErrorInvalidValue;
+  if (w.bits == 4) RSTR_QG_R(4);
+  else RSTR_QG_R(8);
+#undef RSTR_QG_R
+#undef RSTR_QG_S
 #undef RSTR_QG
   return hipGetLastError();
+}
+
+__device__ __forceinline__ f4 sl_load4(const Slices& s, size_t i) {
+  const f4 a = *reinterpret_cast<const f4*>(s.p + i);
+  if (s.n == 1) return a;
+  const f4 b = *reinterpret_cast<const f4*>(s.p + s.stride + i);
+  f4 r;
+  if (s.n == 2) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = a[k] + b[k];
+    return r;
+  }
+  const f4 c = *reinterpret_cast<const f4*>(s.p + 2 * s.stride + i);
+  const f4 d = *reinterpret_cast<const f4*>(s.p + 3 * s.stride + i);
+#pragma unroll
+  for (int k = 0; k < 4; k++) r[k] = (a[k] + b[k]) + (c[k] + d[k]);
+  return r;
 }
 
 // ===========================================================================
@@ -385,21 +503,31 @@ hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, floa
 // The same kernel serves the post-ffn step: xout = xmid + (rms(dn, pffln) | dn)
 // followed by the next layer's input norm (or the final norm of the head).
 __global__ __launch_bounds__(256) void k_residual_norm_quant(
-    const float* __restrict__ o, const float* __restrict__ x, float* __restrict__ xout,
+    Slices o, const float* __restrict__ x, float* __restrict__ xout,
     const float* __restrict__ post, const float* __restrict__ gnext, float goff, float eps, int rows,
     int n, _Float16* __restrict__ Q, float* __restrict__ S, int mpad) {
   int lane = threadIdx.x & 63;
   int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   int n4 = n >> 2, nb = n >> 5;
-  const float* orow = o + (size_t)row * n;
+  const size_t orow = (size_t)row * n;
   const float* xr = x + (size_t)row * n;
   float* xo = xout + (size_t)row * n;
   float r1 = 1.0f;
-  if (post) r1 = rms_scale(row_sumsq(orow, n4, lane), n, eps);
+  if (post) {
+    float a = 0.0f;
+    for (int c = lane; c < n4; c += 64) {
+      f4 v = sl_load4(o, orow + 4 * c);
+      a = __builtin_fmaf(v[0], v[0], a);
+      a = __builtin_fmaf(v[1], v[1], a);
+      a = __builtin_fmaf(v[2], v[2], a);
+      a = __builtin_fmaf(v[3], v[3], a);
+    }
+    r1 = rms_scale(wave_tree_sum(a), n, eps);
+  }
   float acc = 0.0f;
   for (int c = lane; c < n4; c += 64) {
-    f4 ov = *reinterpret_cast<const f4*>(orow + 4 * c);
+    f4 ov = sl_load4(o, orow + 4 * c);
     f4 xv = *reinterpret_cast<const f4*>(xr + 4 * c);
     if (post) {
       f4 pg = *reinterpret_cast<const f4*>(post + 4 * c);
@@ -429,7 +557,7 @@ __global__ __launch_bounds__(256) void k_residual_norm_quant(
   }
 }
 
-hipError_t launch_post_attn(hipStream_t st, const float* o, const float* x, float* xmid,
+hipError_t launch_post_attn(hipStream_t st, Slices o, const float* x, float* xmid,
                             const float* paln, const float* pfln, float goff, float eps, int rows,
                             int n, ActBuf& out) {
   hipLaunchKernelGGL(k_residual_norm_quant, dim3((rows + 3) / 4), dim3(256), 0, st, o, x, xmid, paln,
@@ -437,7 +565,7 @@ hipError_t launch_post_attn(hipStream_t st, const float* o, const float* x, floa
   return hipGetLastError();
 }
 
-hipError_t launch_post_ffn(hipStream_t st, const float* dn, const float* xmid, float* xout,
+hipError_t launch_post_ffn(hipStream_t st, Slices dn, const float* xmid, float* xout,
                            const float* pffln, const float* gnext, float goff, float eps, int rows,
                            int n, ActBuf& out) {
   hipLaunchKernelGGL(k_residual_norm_quant, dim3((rows + 3) / 4), dim3(256), 0, st, dn, xmid, xout,
@@ -446,21 +574,21 @@ hipError_t launch_post_ffn(hipStream_t st, const float* dn, const float* xmid, f
 }
 
 // hh = act(gate) * up (gelu-mul! / silu-mul!), quantised for the down projection.
-__global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ gu, int rows, int ff,
+__global__ __launch_bounds__(256) void k_act_quant(Slices gu, int rows, int ff,
                                                    int geglu, _Float16* __restrict__ Q,
                                                    float* __restrict__ S, int mpad) {
   int lane = threadIdx.x & 63;
   int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* gr = gu + (size_t)row * 2 * ff;
+  const size_t gr = (size_t)row * 2 * ff;
   int n4 = ff >> 2, nb = ff >> 5;
   for (int c0 = 0; c0 < n4; c0 += 64) {
     int c = c0 + lane;
     bool valid = c < n4;
     f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
     if (valid) {
-      f4 gv = *reinterpret_cast<const f4*>(gr + 4 * c);
-      f4 uv = *reinterpret_cast<const f4*>(gr + ff + 4 * c);
+      f4 gv = sl_load4(gu, gr + 4 * c);
+      f4 uv = sl_load4(gu, gr + ff + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; i++) y[i] = (geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
     }
@@ -468,7 +596,7 @@ __global__ __launch_bounds__(256) void k_act_quant(const float* __restrict__ gu,
   }
 }
 
-hipError_t launch_act_quant(hipStream_t st, const float* gu, int rows, int ff, int geglu,
+hipError_t launch_act_quant(hipStream_t st, Slices gu, int rows, int ff, int geglu,
                             ActBuf& out) {
   hipLaunchKernelGGL(k_act_quant, dim3((rows + 3) / 4), dim3(256), 0, st, gu, rows, ff, geglu, out.q,
                      out.s, out.mpad);
@@ -480,7 +608,7 @@ hipError_t launch_act_quant(hipStream_t st, const float* gu, int rows, int ff, i
 // then q -> qr (f32), k -> fp16 page slot, v -> fp16 page slot (slot -1 skips).
 // (decoder_gpu.clj layer-form steps qk-norm, rope-pos-rows-buf!, and the
 // routed append of paged_append.clj:179-228.)
-__global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ y, int n_q, int n_kv,
+__global__ __launch_bounds__(64) void k_qkv_post(Slices y, int n_q, int n_kv,
                                                  int hd, const float* __restrict__ qn,
                                                  const float* __restrict__ kn, float goff, float eps,
                                                  const float* __restrict__ cos_t,
@@ -494,16 +622,16 @@ __global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ y, in
   int row = blockIdx.x / nh, hh = blockIdx.x % nh;
   int lane = threadIdx.x;
   int qd = n_q * hd, kvr = n_kv * hd, ncols = qd + 2 * kvr;
-  const float* yr = y + (size_t)row * ncols;
+  const size_t yr = (size_t)row * ncols;
   int slot = slots[row];
   int hd4 = hd >> 2;
   if (hh >= n_q + n_kv) {
     if (slot < 0) return;
     int j = hh - n_q - n_kv;
-    const float* src = yr + qd + kvr + j * hd;
+    const size_t src = yr + qd + kvr + j * hd;
     uint16_t* dst = vp + (size_t)slot * kvr + j * hd;
     for (int c = lane; c < hd4; c += 64) {
-      f4 v = *reinterpret_cast<const f4*>(src + 4 * c);
+      f4 v = sl_load4(y, src + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; i++) dst[4 * c + i] = f2h_bits(v[i]);
     }
@@ -511,12 +639,22 @@ __global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ y, in
   }
   bool is_q = hh < n_q;
   if (!is_q && slot < 0) return;
-  const float* src = is_q ? yr + hh * hd : yr + qd + (hh - n_q) * hd;
+  const size_t src = is_q ? yr + hh * hd : yr + qd + (hh - n_q) * hd;
   const float* gn = is_q ? qn : kn;
   float r = 1.0f;
-  if (gn) r = rms_scale(row_sumsq(src, hd4, lane), hd, eps);
+  if (gn) {
+    float a = 0.0f;
+    for (int c = lane; c < hd4; c += 64) {
+      f4 v = sl_load4(y, src + 4 * c);
+      a = __builtin_fmaf(v[0], v[0], a);
+      a = __builtin_fmaf(v[1], v[1], a);
+      a = __builtin_fmaf(v[2], v[2], a);
+      a = __builtin_fmaf(v[3], v[3], a);
+    }
+    r = rms_scale(wave_tree_sum(a), hd, eps);
+  }
   for (int c = lane; c < hd4; c += 64) {
-    f4 v = *reinterpret_cast<const f4*>(src + 4 * c);
+    f4 v = sl_load4(y, src + 4 * c);
     if (gn) {
       f4 gg = *reinterpret_cast<const f4*>(gn + 4 * c);
 #pragma unroll
@@ -546,7 +684,7 @@ __global__ __launch_bounds__(64) void k_qkv_post(const float* __restrict__ y, in
   }
 }
 
-hipError_t launch_qkv_post(hipStream_t st, const float* yqkv, int rows, int n_q, int n_kv, int hd,
+hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n_kv, int hd,
                            const float* qn, const float* kn, float goff, float eps,
                            const float* cos_t, const float* sin_t, const int32_t* positions,
                            const int32_t* slots, float* qr, uint16_t* kpages, uint16_t* vpages) {
@@ -984,33 +1122,47 @@ hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64
   return hipGetLastError();
 }
 
-// Synthetic K/V for listed pages in every layer: the stand-in for a restored
-// prefix.  Value = fp16(Irwin-Hall(12) N(0,1)) keyed by (seed, layer, slab)
-// and the physical element index, identical to the CPU restatement.
-__global__ void k_fill_synthetic(uint16_t* const* __restrict__ slabs, int n_layers, int64_t pe,
-                                 const int32_t* __restrict__ pages, uint64_t seed) {
-  const int nsl = 2 * n_layers;
-  const int pi = blockIdx.y;
-  const int s = blockIdx.x % nsl;
-  const int chunk = blockIdx.x / nsl;
+// Synthetic K/V, the stand-in for a restored prefix.  For each (layer, slab)
+// RSTR_SYNTH_TEMPLATES page templates hold fp16(Irwin-Hall(12) N(0,1)) values
+// keyed by (seed, layer, slab) and (template*page_elems + element); physical
+// page p copies template (splitmix64(seed ^ p) >> 32) % RSTR_SYNTH_TEMPLATES.
+// Filling is then a bandwidth-bound copy.
+__global__ void k_gen_templates(uint16_t* __restrict__ tmpl, int n_layers, int64_t pe, uint64_t seed) {
+  const int s = blockIdx.y;                       // slab index = slab*L + layer
   const int layer = s % n_layers, slab = s / n_layers;
   const uint64_t key = tensor_key(seed, layer, 64 + slab);
+  const int64_t total = (int64_t)RSTR_SYNTH_TEMPLATES * pe;
+  uint16_t* base = tmpl + (size_t)s * total;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x)
+    base[i] = f2h_bits(synth_normal(key, (uint64_t)i, 0.0, 1.0));
+}
+
+hipError_t launch_gen_templates(hipStream_t st, uint16_t* tmpl, int n_layers, int64_t page_elems,
+                                uint64_t seed) {
+  hipLaunchKernelGGL(k_gen_templates, dim3(256, 2 * n_layers), dim3(256), 0, st, tmpl, n_layers,
+                     page_elems, seed);
+  return hipGetLastError();
+}
+
+__global__ void k_fill_synthetic(uint16_t* const* __restrict__ slabs, int nslabs, int64_t pe,
+                                 const uint16_t* __restrict__ tmpl, const int32_t* __restrict__ pages,
+                                 uint64_t seed) {
+  const int pi = blockIdx.y;
+  const int s = blockIdx.x;
   const int64_t page = pages[pi];
-  uint16_t* base = slabs[s];
-  const int64_t e0 = (int64_t)chunk * 4096;
-  for (int64_t e = e0 + threadIdx.x; e < min(pe, e0 + 4096); e += blockDim.x) {
-    const uint64_t idx = (uint64_t)page * (uint64_t)pe + (uint64_t)e;
-    base[idx] = f2h_bits(synth_normal(key, idx, 0.0, 1.0));
-  }
+  const int t = (int)((splitmix64(seed ^ (uint64_t)page) >> 32) % RSTR_SYNTH_TEMPLATES);
+  const uint4* src = reinterpret_cast<const uint4*>(tmpl + ((size_t)s * RSTR_SYNTH_TEMPLATES + t) * pe);
+  uint4* dst = reinterpret_cast<uint4*>(slabs[s] + (size_t)page * pe);
+  for (int64_t i = threadIdx.x; i < pe / 8; i += blockDim.x) dst[i] = src[i];
 }
 
 hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
-                                 int64_t page_elems, const int32_t* pages, int npages,
-                                 uint64_t seed) {
+                                 int64_t page_elems, const uint16_t* tmpl, const int32_t* pages,
+                                 int npages, uint64_t seed) {
   if (npages <= 0) return hipSuccess;
-  const int chunks = (int)((page_elems + 4095) / 4096);
-  hipLaunchKernelGGL(k_fill_synthetic, dim3(2 * n_layers * chunks, npages), dim3(256), 0, st, slabs,
-                     n_layers, page_elems, pages, seed);
+  hipLaunchKernelGGL(k_fill_synthetic, dim3(2 * n_layers, npages), dim3(256), 0, st, slabs,
+                     2 * n_layers, page_elems, tmpl, pages, seed);
   return hipGetLastError();
 }
 

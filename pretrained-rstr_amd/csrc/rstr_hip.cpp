@@ -90,7 +90,27 @@ struct rstr_pool {
   uint16_t** d_slabs = nullptr;
   int32_t* d_pairs = nullptr;
   int32_t* h_pairs = nullptr;             // pinned
+  uint16_t* tmpl = nullptr;               // synthetic-prefix page templates
+  uint64_t tmpl_seed = 0;
+  bool tmpl_ready = false;
 };
+
+// Generate (once per seed) the page templates the synthetic fill copies from.
+static hipError_t ensure_templates(rstr_pool* p, uint64_t seed) {
+  if (p->tmpl_ready && p->tmpl_seed == seed) return hipSuccess;
+  int L = p->m->d.n_layers;
+  if (!p->tmpl) {
+    hipError_t e = hipMalloc(&p->tmpl, sizeof(uint16_t) * (size_t)2 * L * RSTR_SYNTH_TEMPLATES * p->page_elems);
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = launch_gen_templates(p->m->s->stream, p->tmpl, L, p->page_elems, seed);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->m->s->stream);
+  if (e == hipSuccess) {
+    p->tmpl_seed = seed;
+    p->tmpl_ready = true;
+  }
+  return e;
+}
 
 struct StagedDev {                        // one uploaded schedule step
   int64_t desc_off;                       // int32 offset in sched_desc
@@ -99,6 +119,8 @@ struct StagedDev {                        // one uploaded schedule step
   uint64_t fill_seed;
   int64_t cow_off;
   int32_t n_cow;
+  int64_t prime_off;
+  int32_t n_prime;
 };
 
 struct rstr_decoder {
@@ -106,6 +128,7 @@ struct rstr_decoder {
   rstr_pool* p = nullptr;
   int B = 0, pps = 0, maxpos = 0, split = 0, mpad = 0, kmax = 0, max_items = 0;
   int qd = 0, kvr = 0, nqkv = 0;
+  int s_qkv = 1, s_o = 1, s_gu = 1, s_down = 1;   // split-K slices per projection
   // device state / scratch
   float *r0 = nullptr, *xmid = nullptr, *o = nullptr, *yqkv = nullptr, *qr = nullptr;
   float *gu = nullptr, *logits = nullptr, *part = nullptr;
@@ -163,6 +186,16 @@ extern "C" int rstr_session_close(rstr_session* s) {
 }
 
 extern "C" const char* rstr_last_error(const rstr_session* s) { return s ? s->err.c_str() : ""; }
+
+extern "C" int rstr_session_memory(rstr_session* s, int64_t* free_bytes, int64_t* total_bytes) {
+  if (!s) return fail(nullptr, RSTR_E_INVALID, "null session");
+  HIPCHK(s, hipSetDevice(s->device));
+  size_t f = 0, t = 0;
+  HIPCHK(s, hipMemGetInfo(&f, &t));
+  if (free_bytes) *free_bytes = (int64_t)f;
+  if (total_bytes) *total_bytes = (int64_t)t;
+  return RSTR_OK;
+}
 extern "C" const char* rstr_open_error(void) { return g_open_err.c_str(); }
 
 // ---------------------------------------------------------------------------
@@ -539,6 +572,7 @@ extern "C" int rstr_pool_close(rstr_pool* p) {
   hipFree(p->d_slabs);
   hipFree(p->d_pairs);
   hipHostFree(p->h_pairs);
+  if (p->tmpl) hipFree(p->tmpl);
   delete p;
   return RSTR_OK;
 }
@@ -602,9 +636,11 @@ extern "C" int rstr_pool_fill_synthetic(rstr_pool* p, const int32_t* pages, int3
   HIPCHK(s, hipSetDevice(s->device));
   int32_t* d = nullptr;
   HIPCHK(s, dmalloc(&d, n));
-  hipError_t e = hipMemcpy(d, pages, sizeof(int32_t) * n, hipMemcpyHostToDevice);
+  hipError_t e = ensure_templates(p, seed);
+  if (e == hipSuccess) e = hipMemcpy(d, pages, sizeof(int32_t) * n, hipMemcpyHostToDevice);
   if (e == hipSuccess)
-    e = launch_fill_synthetic(s->stream, p->d_slabs, p->m->d.n_layers, p->page_elems, d, n, seed);
+    e = launch_fill_synthetic(s->stream, p->d_slabs, p->m->d.n_layers, p->page_elems, p->tmpl, d, n,
+                              seed);
   if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
   hipFree(d);
   HIPCHK(s, e);
@@ -655,6 +691,11 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   d->kvr = md.n_kv * md.head_dim;
   d->nqkv = d->qd + 2 * d->kvr;
   d->kmax = std::max(md.d_model, std::max(d->qd, md.d_ff));
+  d->s_qkv = qgemm_splits(d->nqkv, d->mpad);
+  d->s_o = qgemm_splits(md.d_model, d->mpad);
+  d->s_gu = qgemm_splits(2 * md.d_ff, d->mpad);
+  d->s_down = qgemm_splits(md.d_model, d->mpad);
+  const int s_d = std::max(d->s_o, d->s_down);
   int64_t max_pos_tokens = std::min<int64_t>((int64_t)pps * p->page_size, (int64_t)maxpos + 1);
   int64_t splits = (max_pos_tokens + split - 1) / split + 1;
   d->max_items = (int)std::min<int64_t>((int64_t)batch * md.n_kv * splits, INT32_MAX / 4);
@@ -671,10 +712,10 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   auto A = [&](hipError_t x) { if (e == hipSuccess) e = x; };
   A(dmalloc(&d->r0, (size_t)d->mpad * md.d_model));
   A(dmalloc(&d->xmid, (size_t)d->mpad * md.d_model));
-  A(dmalloc(&d->o, (size_t)d->mpad * md.d_model));
-  A(dmalloc(&d->yqkv, (size_t)batch * d->nqkv));
+  A(dmalloc(&d->o, (size_t)s_d * batch * md.d_model));
+  A(dmalloc(&d->yqkv, (size_t)d->s_qkv * batch * d->nqkv));
   A(dmalloc(&d->qr, (size_t)batch * d->qd));
-  A(dmalloc(&d->gu, (size_t)batch * 2 * md.d_ff));
+  A(dmalloc(&d->gu, (size_t)d->s_gu * batch * 2 * md.d_ff));
   A(dmalloc(&d->logits, (size_t)batch * md.vocab));
   A(dmalloc(&d->part, (size_t)d->max_items * G * (md.head_dim + 2)));
   A(dmalloc(&d->rope_cos, (size_t)2 * maxpos * half));
@@ -907,9 +948,10 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
     const int half = hd / 2;
     uint16_t* kp = d->p->slabs[l];
     uint16_t* vp = d->p->slabs[L + l];
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.qkv, d->act, B, d->yqkv, d->nqkv); });
+    const size_t sq = (size_t)B * d->nqkv, sd = (size_t)B * dm, sg = (size_t)B * 2 * md.d_ff;
+    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.qkv, d->act, B, d->yqkv, d->nqkv, d->s_qkv, sq); });
     run(RSTR_K_QKV_POST, [&] {
-      return launch_qkv_post(st, d->yqkv, B, md.n_q, md.n_kv, hd, W.q_norm, W.k_norm, goff, md.eps,
+      return launch_qkv_post(st, Slices{d->yqkv, d->s_qkv, sq}, B, md.n_q, md.n_kv, hd, W.q_norm, W.k_norm, goff, md.eps,
                              d->rope_cos + (size_t)ti * d->maxpos * half,
                              d->rope_sin + (size_t)ti * d->maxpos * half, pos, slots, d->qr, kp, vp);
     });
@@ -920,20 +962,24 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
     run(RSTR_K_ATTN_MERGE, [&] {
       return launch_attn_merge(st, geo[wi], len, d->lane_tab + wi * tabw, d->part, nullptr, &d->act);
     });
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.o, d->act, B, d->o, dm); });
+    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.o, d->act, B, d->o, dm, d->s_o, sd); });
     run(RSTR_K_ROWS, [&] {
-      return launch_post_attn(st, d->o, d->r0, d->xmid, W.post_attn_norm, W.ffn_pre_norm, goff, md.eps, B,
+      return launch_post_attn(st, Slices{d->o, d->s_o, sd}, d->r0, d->xmid, W.post_attn_norm, W.ffn_pre_norm, goff, md.eps, B,
                               dm, d->act);
     });
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.gu, d->act, B, d->gu, 2 * md.d_ff); });
-    run(RSTR_K_ROWS, [&] { return launch_act_quant(st, d->gu, B, md.d_ff, md.ffn_geglu, d->act); });
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm); });
+    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.gu, d->act, B, d->gu, 2 * md.d_ff, d->s_gu, sg); });
+    run(RSTR_K_ROWS, [&] {
+      return launch_act_quant(st, Slices{d->gu, d->s_gu, sg}, B, md.d_ff, md.ffn_geglu, d->act);
+    });
+    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm, d->s_down, sd); });
     const float* gnext = (l + 1 < L) ? d->m->layers[l + 1].attn_norm : d->m->final_norm;
     run(RSTR_K_ROWS, [&] {
-      return launch_post_ffn(st, d->o, d->xmid, d->r0, W.ffn_post_norm, gnext, goff, md.eps, B, dm, d->act);
+      return launch_post_ffn(st, Slices{d->o, d->s_down, sd}, d->xmid, d->r0, W.ffn_post_norm, gnext, goff, md.eps, B, dm, d->act);
     });
   }
-  run(RSTR_K_HEAD, [&] { return launch_qgemm(st, d->m->head, d->act, B, d->logits, md.vocab); });
+  run(RSTR_K_HEAD, [&] {
+    return launch_qgemm(st, d->m->head, d->act, B, d->logits, md.vocab, 1, (size_t)B * md.vocab);
+  });
   run(RSTR_K_TAIL, [&] {
     return launch_argmax_gather(st, d->logits, B, md.vocab, d->m->emb, dm, d->tokbuf, d->r0);
   });
@@ -993,6 +1039,8 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
   rstr_session* s = d->m->s;
   if (n <= 0 || !steps) return fail(s, RSTR_E_INVALID, "empty schedule");
   int64_t words = 0, pages = 0;
+  uint64_t fill_seed = 0;
+  bool fill_seed_set = false;
   for (int32_t i = 0; i < n; i++) {
     const auto& t = steps[i];
     int rc = validate_step(d, t.slots, t.row_offsets, t.positions, t.page_table, t.lengths,
@@ -1000,6 +1048,18 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
     if (rc) return rc;
     if (t.n_fill < 0 || t.n_cow < 0 || (t.n_fill && !t.fill_pages) || (t.n_cow && !t.cow_pairs))
       return fail(s, RSTR_E_INVALID, "invalid staged fill or copy list");
+    if (t.n_prime < 0 || t.n_prime > d->B || (t.n_prime && (!t.prime_lanes || !t.prime_tokens)))
+      return fail(s, RSTR_E_INVALID, "invalid staged prime list");
+    if (int rc2 = check_lanes(d, t.n_prime, t.prime_lanes)) return rc2;
+    for (int32_t j = 0; j < t.n_prime; j++)
+      if (t.prime_tokens[j] < 0 || t.prime_tokens[j] >= d->m->d.vocab)
+        return fail(s, RSTR_E_INVALID, "staged prime token out of range");
+    if (t.n_fill && fill_seed_set && t.fill_seed != fill_seed)
+      return fail(s, RSTR_E_INVALID, "one schedule uses one synthetic fill seed");
+    if (t.n_fill) {
+      fill_seed = t.fill_seed;
+      fill_seed_set = true;
+    }
     for (int32_t j = 0; j < t.n_fill; j++)
       if (t.fill_pages[j] < 0 || t.fill_pages[j] >= d->p->physical_pages)
         return fail(s, RSTR_E_INVALID, "staged fill page out of range");
@@ -1007,10 +1067,11 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
       if (t.cow_pairs[j] < 0 || t.cow_pairs[j] >= d->p->physical_pages)
         return fail(s, RSTR_E_INVALID, "staged copy page out of range");
     words += d->desc_words;
-    pages += t.n_fill + 2 * t.n_cow;
+    pages += t.n_fill + 2 * t.n_cow + 2 * t.n_prime;
   }
   HIPCHK(s, hipSetDevice(s->device));
   HIPCHK(s, hipStreamSynchronize(s->stream));
+  if (fill_seed_set) HIPCHK(s, ensure_templates(d->p, fill_seed));
   if (words > d->sched_desc_cap) {
     if (d->sched_desc) hipFree(d->sched_desc);
     d->sched_desc = nullptr;
@@ -1048,6 +1109,11 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
     sd.n_cow = t.n_cow;
     std::memcpy(hpages.data() + po, t.cow_pairs, sizeof(int32_t) * 2 * t.n_cow);
     po += 2 * t.n_cow;
+    sd.prime_off = po;
+    sd.n_prime = t.n_prime;
+    std::memcpy(hpages.data() + po, t.prime_lanes, sizeof(int32_t) * t.n_prime);
+    std::memcpy(hpages.data() + po + t.n_prime, t.prime_tokens, sizeof(int32_t) * t.n_prime);
+    po += 2 * t.n_prime;
     d->sched.push_back(sd);
   }
   HIPCHK(s, hipMemcpy(d->sched_desc, hdesc.data(), sizeof(int32_t) * words, hipMemcpyHostToDevice));
@@ -1064,11 +1130,14 @@ static int sched_range(rstr_decoder* d, int32_t first, int32_t count) {
 static hipError_t enqueue_staged_prelude(rstr_decoder* d, const StagedDev& sd, hipStream_t st) {
   hipError_t e = hipSuccess;
   if (sd.n_fill)
-    e = launch_fill_synthetic(st, d->p->d_slabs, d->m->d.n_layers, d->p->page_elems,
+    e = launch_fill_synthetic(st, d->p->d_slabs, d->m->d.n_layers, d->p->page_elems, d->p->tmpl,
                               d->sched_pages + sd.fill_off, sd.n_fill, sd.fill_seed);
   if (e == hipSuccess && sd.n_cow)
     e = launch_copy_pages(st, d->p->d_slabs, 2 * d->m->d.n_layers, d->p->page_elems,
                           d->sched_pages + sd.cow_off, sd.n_cow);
+  if (e == hipSuccess && sd.n_prime)
+    e = launch_gather_rows(st, d->m->emb, d->m->d.d_model, d->sched_pages + sd.prime_off,
+                           d->sched_pages + sd.prime_off + sd.n_prime, sd.n_prime, d->r0);
   if (e == hipSuccess)
     e = hipMemcpyAsync(d->desc, d->sched_desc + sd.desc_off, sizeof(int32_t) * d->desc_words,
                        hipMemcpyDeviceToDevice, st);

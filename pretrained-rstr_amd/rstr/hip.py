@@ -22,6 +22,7 @@ KERNEL_CLASSES = ("qgemm", "head", "attn_split", "attn_merge", "qkv_post", "rows
 
 EXPORTS = (
     "rstr_session_open", "rstr_session_close", "rstr_last_error", "rstr_open_error",
+    "rstr_session_memory",
     "rstr_model_bind", "rstr_model_bind_synthetic", "rstr_model_close", "rstr_model_weight_bytes",
     "rstr_model_export_linear", "rstr_pool_open", "rstr_pool_close", "rstr_pool_copy_page",
     "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_decoder_open",
@@ -58,7 +59,8 @@ class StagedStep(C.Structure):
                 ("page_table", C.c_void_p), ("lengths", C.c_void_p),
                 ("start_positions", C.c_void_p), ("fill_pages", C.c_void_p),
                 ("n_fill", C.c_int32), ("fill_seed", C.c_uint64), ("cow_pairs", C.c_void_p),
-                ("n_cow", C.c_int32)]
+                ("n_cow", C.c_int32), ("prime_lanes", C.c_void_p), ("prime_tokens", C.c_void_p),
+                ("n_prime", C.c_int32)]
 
 
 _lib = None
@@ -77,6 +79,7 @@ def lib():
             "rstr_session_close": (i32, [P]),
             "rstr_last_error": (C.c_char_p, [P]),
             "rstr_open_error": (C.c_char_p, []),
+            "rstr_session_memory": (i32, [P, C.POINTER(i64), C.POINTER(i64)]),
             "rstr_model_bind": (i32, [P, P, P, i32, C.POINTER(P)]),
             "rstr_model_bind_synthetic": (i32, [P, P, u64, C.POINTER(P)]),
             "rstr_model_close": (i32, [P]),
@@ -140,6 +143,16 @@ class Session:
         if rc != 0:
             raise RstrError(rc, lib().rstr_open_error().decode())
         self.h = h
+        self.children = []   # open models, pools, decoders (closed before the session)
+
+    def _adopt(self, obj):
+        self.children.append(obj)
+
+    def memory(self):
+        """(free, total) device bytes."""
+        f, t = C.c_int64(), C.c_int64()
+        self.check(lib().rstr_session_memory(self.h, C.byref(f), C.byref(t)))
+        return f.value, t.value
 
     def check(self, rc: int):
         if rc != 0:
@@ -147,6 +160,10 @@ class Session:
 
     def close(self):
         if self.h:
+            order = {"Decoder": 0, "Pool": 1, "Model": 2}
+            for obj in sorted(self.children, key=lambda o: order.get(type(o).__name__, 3)):
+                obj.close()
+            self.children = []
             lib().rstr_session_close(self.h)
             self.h = None
 
@@ -178,6 +195,7 @@ class Model:
                                        len(tensors), C.byref(h))
         sess.check(rc)
         self.h = h
+        sess._adopt(self)
 
     @property
     def weight_bytes(self) -> int:
@@ -213,6 +231,7 @@ class Pool:
         h = C.c_void_p()
         self.sess.check(lib().rstr_pool_open(model.h, page_size, physical_pages, C.byref(h)))
         self.h = h
+        self.sess._adopt(self)
 
     @property
     def page_elems(self) -> int:
@@ -299,6 +318,7 @@ class Decoder:
                                                 C.byref(h)))
         self.h = h
         self._keep = []
+        self.sess._adopt(self)
 
     def set_graph(self, enabled: bool):
         self.sess.check(lib().rstr_decoder_set_graph(self.h, 1 if enabled else 0))
@@ -340,12 +360,16 @@ class Decoder:
                 f[k] = a.ctypes.data
             fill = _i32(st.get("fill_pages", []))
             cow = _i32(st.get("cow_pairs", np.zeros((0, 2))))
-            keep += [fill, cow]
+            pl = _i32(st.get("prime_lanes", []))
+            ptk = _i32(st.get("prime_tokens", []))
+            keep += [fill, cow, pl, ptk]
             arr[i] = StagedStep(f["slots"], f["row_offsets"], f["positions"], f["page_table"],
                                 f["lengths"], f["start_positions"],
                                 fill.ctypes.data if fill.size else None, fill.size,
                                 int(st.get("fill_seed", 0)),
-                                cow.ctypes.data if cow.size else None, cow.size // 2)
+                                cow.ctypes.data if cow.size else None, cow.size // 2,
+                                pl.ctypes.data if pl.size else None,
+                                ptk.ctypes.data if ptk.size else None, pl.size)
         self.sess.check(lib().rstr_schedule_upload(self.h, C.cast(arr, C.c_void_p), len(steps)))
         self._keep = keep
 

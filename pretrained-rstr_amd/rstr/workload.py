@@ -1,0 +1,160 @@
+"""Synthetic continuous-batching workloads, planned through the control-plane
+mirror into device-resident step schedules.
+
+The planner admits requests into fixed decode lanes the way the reference's
+worker does (``src/pretrained/continuation/worker.clj:12-111``: retain running
+lanes, refill free lanes from the queue, retire on length): each admission
+reserves projected capacity (prompt + output, ``residency.clj:159-179`` /
+``page_pool.clj:567-611``), allocates the route for the restored prefix (KV
+holds prompt-1 rows, the last prompt token is the pending input,
+``continuation.clj:1-8``), fills its pages with synthetic fp16 K/V (standing in
+for a restored prefix) and primes the lane.  Every step then goes through
+``PagedDecoder.step_lanes`` with a recording device, which captures the exact
+descriptors, copy-on-write copies and primes the GPU will replay.
+"""
+from __future__ import annotations
+
+import collections
+import time
+
+import numpy as np
+
+from .page_pool import PagePool, PagePoolError
+from .paged_decoder import PagedDecoder
+
+
+class RecordingDevice:
+    """Device protocol implementation that records instead of executing."""
+
+    def __init__(self):
+        self.cur = None
+
+    def begin(self):
+        self.cur = {"fill_pages": [], "cow_pairs": [], "prime_lanes": [], "prime_tokens": []}
+
+    def end(self):
+        st, self.cur = self.cur, None
+        return st
+
+    def copy_page(self, src, dst):
+        self.cur["cow_pairs"].append((src, dst))
+
+    def fill(self, pages):
+        self.cur["fill_pages"].extend(int(p) for p in pages)
+
+    def prime_rows(self, lane_tokens):
+        for lt in lane_tokens:
+            self.cur["prime_lanes"].append(int(lt["lane"]))
+            self.cur["prime_tokens"].append(int(lt["token"]))
+
+    def upload(self, desc):
+        self.cur.update({k: np.array(v, np.int32) for k, v in desc.items()})
+
+    def run(self):
+        pass
+
+    def download_tokens(self):
+        return np.zeros(len(self.cur["slots"]), np.int32)
+
+
+class ChurnPlanner:
+    """Poisson arrivals, uniform prompt/output lengths, fixed lanes, fixed page pool."""
+
+    def __init__(self, cfg: dict, batch: int, page_size: int, physical_pages: int, maxpos: int,
+                 seed: int, arrival_mean: float = 4.0, prompt=(128, 4096), output=(32, 512),
+                 fill_seed: int = 7, warm_start: bool = True):
+        self.cfg, self.batch, self.maxpos = cfg, batch, maxpos
+        self.rng = np.random.default_rng(seed)
+        self.arrival_mean, self.prompt, self.output = arrival_mean, prompt, output
+        self.fill_seed = fill_seed
+        self.rec = RecordingDevice()
+        self.pool = PagePool(page_size, physical_pages, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"],
+                             device=self.rec)
+        self.dec = PagedDecoder(self.pool, self.rec, batch_size=batch, maxpos=maxpos)
+        self.lanes = [None] * batch
+        self.queue = collections.deque()
+        self.next_id = 0
+        self.warm_start = warm_start
+        self.steps_planned = 0
+        self.host_seconds = 0.0
+        self.retired = 0
+        self.rejected_admissions = 0
+
+    def _arrive(self, n):
+        for _ in range(n):
+            p = int(self.rng.integers(self.prompt[0], self.prompt[1] + 1))
+            o = int(self.rng.integers(self.output[0], self.output[1] + 1))
+            self.queue.append({"id": self.next_id, "prompt": p, "output": o,
+                               "token": int(self.rng.integers(0, self.cfg["vocab"]))})
+            self.next_id += 1
+
+    def _admit(self, lane, req, progress=0):
+        cid = req["id"]
+        try:
+            cap = self.pool.reserve_capacity(cid, req["prompt"] + req["output"])
+        except PagePoolError:
+            self.rejected_admissions += 1
+            return False
+        route = self.pool.allocate_route(cid, req["prompt"] - 1 + progress, capacity_reservation=cap)
+        self.rec.fill(route.pages)
+        self.dec.prime_lanes([{"lane": lane, "token": req["token"]}])
+        self.lanes[lane] = {"cid": cid, "cap": cap, "left": req["output"] - progress}
+        return True
+
+    def plan_step(self) -> dict:
+        t0 = time.perf_counter()
+        self.rec.begin()
+        if self.steps_planned == 0 and self.warm_start:
+            # steady-state start: every lane holds a request part-way through its output
+            self._arrive(self.batch)
+            for lane in range(self.batch):
+                req = self.queue.popleft()
+                self._admit(lane, req, progress=int(self.rng.integers(0, req["output"])))
+        self._arrive(int(self.rng.poisson(self.arrival_mean)))
+        for lane in range(self.batch):
+            if self.lanes[lane] is None and self.queue:
+                if not self._admit(lane, self.queue[0]):
+                    break
+                self.queue.popleft()
+        work = []
+        for lane, st in enumerate(self.lanes):
+            if st is not None:
+                r = self.pool.route(st["cid"])
+                work.append({"lane": lane, "continuation_id": st["cid"],
+                             "position": r.start_position + r.token_count})
+        self.dec.step_lanes(work)
+        for lane, st in enumerate(self.lanes):
+            if st is None:
+                continue
+            st["left"] -= 1
+            if st["left"] <= 0:
+                self.pool.release_route(st["cid"])
+                self.pool.release_capacity(st["cap"])
+                self.lanes[lane] = None
+                self.retired += 1
+        out = self.rec.end()
+        out["fill_seed"] = self.fill_seed
+        out["active"] = len(work)
+        self.steps_planned += 1
+        self.host_seconds += time.perf_counter() - t0
+        return out
+
+
+def step_bytes(cfg: dict, step: dict, weight_bytes: int) -> dict:
+    """Algorithmic HBM bytes of one decode step: packed weights once, the visible
+    fp16 K+V of every layer (window-limited on local layers; logical rows, which
+    equal unique rows when no pages are shared), fp16 appends, embedding gather."""
+    L, kvr, d = cfg["n_layers"], cfg["n_kv"] * cfg["head_dim"], cfg["d_model"]
+    lengths = np.asarray(step["lengths"], np.int64)
+    active = lengths > 0
+    per_layer_kv = []
+    for layer in range(L):
+        glob = cfg["global_pattern"] <= 0 or (layer + 1) % cfg["global_pattern"] == 0
+        w = cfg["sliding_window"] if (cfg["sliding_window"] > 0 and not glob) else 0
+        vis = np.minimum(lengths, w) if w else lengths
+        per_layer_kv.append(int(vis.sum()) * kvr * 2 * 2)
+    kv = sum(per_layer_kv)
+    appends = int(active.sum()) * L * kvr * 2 * 2
+    gather = int(active.sum()) * d * 4
+    return {"weights": weight_bytes, "kv": kv, "kv_per_layer": per_layer_kv, "appends": appends,
+            "gather": gather, "total": weight_bytes + kv + appends + gather}

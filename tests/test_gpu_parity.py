@@ -262,6 +262,16 @@ def _run_lanes(sess, cfg, B, prefix, schedule, graph=True, split=16, ps=16, page
     d.set_graph(graph)
     om = O.Model(cfg, seed=seed)
     od = O.Decoder(om, B, ps, pages, pps, maxpos, kv_f16=True, split=split)
+    r = dict(m=m, p=p, d=d, om=om, od=od, routes=routes)
+    try:
+        return _drive(r, cfg, B, prefix, schedule, kv_seed, tokens)
+    except BaseException:
+        _close(r)
+        raise
+
+
+def _drive(r, cfg, B, prefix, schedule, kv_seed, tokens):
+    m, p, d, om, od, routes = r["m"], r["p"], r["d"], r["om"], r["od"], r["routes"]
     for b, n in enumerate(prefix):
         new = routes.prefix(b, n)
         if new:
@@ -282,7 +292,8 @@ def _run_lanes(sess, cfg, B, prefix, schedule, graph=True, split=16, ps=16, page
         assert np.array_equal(gl[act], ol[act])
         hist_g.append(g)
         hist_o.append(o)
-    return dict(m=m, p=p, d=d, om=om, od=od, routes=routes, g=hist_g, o=hist_o)
+    r.update(g=hist_g, o=hist_o)
+    return r
 
 
 def _close(r):
@@ -326,6 +337,22 @@ def test_lane_results_do_not_depend_on_the_batch(sess):
     finally:
         _close(big)
         _close(one)
+
+
+@pytest.mark.parametrize("B", [40, 100, 130])
+def test_wide_batches_bit_exact(sess, B):
+    """Row-tile groupings of the projection kernel (1, 2 and 3 row groups of up to
+    128 rows; split-K slices) against the oracle."""
+    print(f"case wide batch B={B}", flush=True)
+    cfg = configs.TINY_QWEN
+    rng = np.random.default_rng(B)
+    prefix = [int(x) for x in rng.integers(0, 40, B)]
+    sched = [list(range(B))] * 2
+    r = _run_lanes(sess, cfg, B, prefix, sched, pages=B * 4 + 8, pps=4, maxpos=60)
+    try:
+        assert np.array_equal(r["d"].rows(), r["od"].r0())
+    finally:
+        _close(r)
 
 
 @pytest.mark.parametrize("name,layers", [("llama3_8b", 1), ("gemma3_270m", 6), ("qwen3_06b", 1)])
