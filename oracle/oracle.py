@@ -162,6 +162,8 @@ def quant_act(x: np.ndarray):
 def qlinear(bits: int, wq: np.ndarray, ws: np.ndarray, xq: np.ndarray, xs: np.ndarray) -> np.ndarray:
     n_out = ws.shape[0]
     rows, k_in = xq.shape
+    if k_in % 128:
+        raise ValueError("input width must be a multiple of 128 (4 quarters of 32-blocks)")
     y = np.empty((rows, n_out), np.float32)
     lib().orc_qlinear(bits, ptr(np.ascontiguousarray(wq)), ptr(np.ascontiguousarray(ws)), n_out, k_in,
                       ptr(np.ascontiguousarray(xq)), ptr(f32(xs)), rows, ptr(y))

@@ -243,12 +243,11 @@ void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float*
 
 /* ------------------------------------------------------------------------ */
 /* Dequantising linear y[r][n] = sum_b isum(r,n,b) * (dw[n,b] * dx[r,b]).    */
-/* Canonical order: the nb blocks form 64 contiguous parts of c=ceil(nb/64) */
-/* blocks (trailing parts may be short or empty); each part accumulates      */
-/* acc = fmaf(isum, dw*dx, acc) in block order from +0; the 64 part sums are */
-/* combined by the balanced pairwise tree in part order.  isum is the exact  */
-/* integer block dot.  Integer dots: pinned by brute force; the whole linear */
-/* is pinned against a float64 numpy restatement within 1e-5 relative.       */
+/* Canonical order: the nb blocks (nb % 4 == 0) form 4 contiguous quarters   */
+/* of nb/4 blocks; each quarter accumulates acc = fmaf(isum, dw*dx, acc) in   */
+/* block order from +0; y = (q0 + q1) + (q2 + q3).  isum is the exact integer */
+/* block dot.  Integer dots: pinned by brute force; the whole linear is       */
+/* pinned against a float64 numpy restatement within 1e-5 relative.          */
 /* ------------------------------------------------------------------------ */
 static inline float tree64(float* v) {
   for (int w = 1; w < 64; w <<= 1)
@@ -273,8 +272,9 @@ static inline int32_t dot_q8(const int8_t* q, const int8_t* x) {
 
 void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out, int32_t k_in,
                  const int8_t* xq, const float* xs, int32_t rows, float* y) {
+  /* precondition: k_in % 128 == 0 (checked by the callers) */
   int32_t nb = k_in / 32;
-  int32_t c = (nb + 63) / 64;
+  int32_t qs = nb / 4;
 #pragma omp parallel for schedule(static)
   for (int32_t n = 0; n < n_out; n++) {
     float dw[nb > 0 ? nb : 1];
@@ -282,21 +282,19 @@ void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out
     for (int32_t r = 0; r < rows; r++) {
       const int8_t* xr = xq + (int64_t)r * k_in;
       const float* sr = xs + (int64_t)r * nb;
-      float part[64];
-      for (int32_t p = 0; p < 64; p++) {
+      float quarter[4];
+      for (int32_t q = 0; q < 4; q++) {
         float acc = 0.0f;
-        int32_t b0 = p * c;
-        int32_t b1 = (int32_t)imin64(nb, (int64_t)b0 + c);
-        for (int32_t b = b0; b < b1; b++) {
+        for (int32_t b = q * qs; b < (q + 1) * qs; b++) {
           int32_t isum = (bits == 4)
                              ? dot_q4((const uint8_t*)wq + ((int64_t)n * nb + b) * 16, xr + 32 * b)
                              : dot_q8((const int8_t*)wq + ((int64_t)n * nb + b) * 32, xr + 32 * b);
           float s = dw[b] * sr[b];
           acc = fmaf((float)isum, s, acc);
         }
-        part[p] = acc;
+        quarter[q] = acc;
       }
-      y[(int64_t)r * n_out + n] = tree64(part);
+      y[(int64_t)r * n_out + n] = (quarter[0] + quarter[1]) + (quarter[2] + quarter[3]);
     }
   }
 }
@@ -304,18 +302,21 @@ void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out
 /* ------------------------------------------------------------------------ */
 /* RMSNorm y = (x * r) * (goff + g), r = 1/sqrt(mean(x^2) + eps)             */
 /* (nn/rms-norm!, decoder_gpu.clj:134-137; decoder.clj:295-300).            */
-/* Canonical sum of squares: element i goes to slot (i/4) mod 64, each slot  */
-/* accumulates fmaf(x,x,acc) in index order, slots combine by the pairwise   */
-/* tree.  Pinned by closed forms and by a float64 numpy restatement.         */
+/* Canonical sum of squares: element i goes to slot (i/4) mod 256, each     */
+/* slot accumulates fmaf(x,x,acc) in index order, the 256 slots combine by   */
+/* the balanced pairwise tree.  Pinned by closed forms and by a float64       */
+/* numpy restatement.                                                        */
 /* ------------------------------------------------------------------------ */
 float orc_sumsq(const float* x, int32_t n) {
-  float slot[64];
-  for (int i = 0; i < 64; i++) slot[i] = 0.0f;
+  float slot[256];
+  for (int i = 0; i < 256; i++) slot[i] = 0.0f;
   for (int32_t i = 0; i < n; i++) {
-    int s = (i >> 2) & 63;
+    int s = (i >> 2) & 255;
     slot[s] = fmaf(x[i], x[i], slot[s]);
   }
-  return tree64(slot);
+  for (int w = 1; w < 256; w <<= 1)
+    for (int i = 0; i < 256; i += 2 * w) slot[i] = slot[i] + slot[i + w];
+  return slot[0];
 }
 
 void orc_rmsnorm(const float* x, const float* g, float gain_offset, float eps, int32_t rows,
@@ -556,7 +557,8 @@ static int desc_ok(const orc_desc* d) {
   if (d->n_layers <= 0 || d->d_model <= 0 || d->d_ff <= 0 || d->n_q <= 0 || d->n_kv <= 0 ||
       d->head_dim <= 0 || d->vocab <= 0)
     return 0;
-  if (d->d_model % 32 || d->d_ff % 32 || (d->n_q * d->head_dim) % 32 || d->head_dim % 8 ||
+  /* every projection input width splits into 4 quarters of whole 32-blocks */
+  if (d->d_model % 128 || d->d_ff % 128 || (d->n_q * d->head_dim) % 128 || d->head_dim % 8 ||
       (d->head_dim & 1) || d->n_q % d->n_kv)
     return 0;
   if (d->weight_bits != 4 && d->weight_bits != 8) return 0;

@@ -8,11 +8,12 @@
 //   Q4 dword  [ct][bq][g][nn][bb]  holds the 8 nibbles of weights
 //             k = 32b + 8g + {0..7}; nibble i carries k_local = {0,2,4,6,1,3,5,7}[i].
 //   Q8 dwords [ct][bq][g][nn][bb][2]; byte i carries k_local = {0,2,1,3,4,6,5,7}[i].
-//   fp16 scales [ct][bq][nn][bb].
+//   fp16 scales [ct][bq][nn/4][bb][nn%4] (a lane whose accumulator holds
+//   columns 4j..4j+3 of a tile reads its 4 blocks' scales as one 32-byte run).
 //   (These permutations make the nibble/byte -> fp16 expansion a mask-or plus
 //   one packed fp16 add; the canonical row-major order is restored on export.)
 //
-//  Quantised activation X[M][K] for the MFMA A operand (Mpad = 16*ceil(M/16)):
+//  Quantised activation X[M][K] for the MFMA B operand (Mpad = 16*ceil(M/16)):
 //   fp16 integer values [Mpad/16][nb][g][m%16][8], fp32 block scales [nb][Mpad].
 //
 //  KV pages per layer and slab: fp16 [page][page_size][n_kv][head_dim]
@@ -50,7 +51,7 @@ struct Slices {
   int n;
   size_t stride;
 };
-int qgemm_splits(int n, int mpad);
+int qgemm_splits(int n, int mpad, int bits);
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride);
 

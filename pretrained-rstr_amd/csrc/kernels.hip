@@ -84,7 +84,7 @@ __global__ void k_gen_linear(uint32_t* __restrict__ W, uint16_t* __restrict__ S,
     }
     scale = f2h_bits(d);
   }
-  S[(((size_t)ct * nb4 + bq) * 16 + nn) * 4 + bb] = scale;
+  S[((((size_t)ct * nb4 + bq) * 4 + (nn >> 2)) * 4 + bb) * 4 + (nn & 3)] = scale;
 }
 
 hipError_t launch_gen_linear(hipStream_t st, const QTensor& t, int col_off, int n_rows, int k,
@@ -138,12 +138,14 @@ hipError_t launch_prescale(hipStream_t st, float* out, const float* in, int64_t 
 // The block dot isum is computed exactly by v_mfma_f32_16x16x32_f16: both
 // operands are small integers (|q_w| <= 8 or 127, |q_x| <= 127) held exactly
 // in fp16, every partial sum is an integer below 2^24, so the fp32 result is
-// the exact integer.  The block combination follows the canonical order:
-// 64 contiguous parts of c = ceil(nb/64) blocks, acc = fmaf(isum, dw*dx, acc)
-// in block order per part, parts combined by the balanced pairwise tree.
-// Wave w of the workgroup owns parts [16w, 16w+16) (a complete level-4
-// subtree, built with a binary-counter stack); the four subtrees meet in LDS
-// as ((w0+w1)+(w2+w3)).
+// the exact integer.  Canonical block order: the nb blocks form 4 contiguous
+// quarters; each quarter accumulates acc = fmaf(isum, dw*dx, acc) in block
+// order from +0; y = (q0 + q1) + (q2 + q3).
+//
+// The MFMA takes the weights as the A operand and the activations as B, so a
+// lane's accumulator holds 4 consecutive output columns (n = 4*(lane/16) + r)
+// of one row (m = lane%16): it needs one activation scale per block and row
+// tile, and the 4 weight scales of its columns per block and column tile.
 
 __device__ __forceinline__ h8 unpack_q4(uint32_t x) {
   const uint32_t M = 0x000F000Fu, E = 0x64006400u;
@@ -168,237 +170,310 @@ __device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1) {
   return r;
 }
 
-// Workgroup: 4 waves.  With RH row halves the waves form CTW = 4/RH column
-// tiles (16 columns each) x RH groups of RT row tiles.  Each wave owns its
-// output tile over the workgroup's whole K range (64/S contiguous parts, a
-// complete subtree of the canonical tree), so it accumulates parts in order and
-// merges leaves with a binary-counter stack.  Activations are staged through a
-// double-buffered LDS ring in chunks of 4 blocks and shared by all waves;
-// weights stream as one 128-bit load per lane per chunk.  With S > 1 the K
-// subtrees land in S output slices that the consumer combines as
-// (s0+s1) or ((s0+s1)+(s2+s3)).
-// Merge leaf `v` into the stack: t1 = trailing ones of the leaf index is the
-// number of completed left siblings.  Written as compile-time recursion so every
-// stack index is a constant before register promotion.
-template <int T, int RT, int LOGP>
-__device__ __forceinline__ void push_rec(int t1, float (&st)[LOGP][RT][4], float (&v)[RT][4],
-                                         float (&fin)[RT][4]) {
-  if constexpr (T == LOGP) {
-#pragma unroll
-    for (int i = 0; i < RT; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) fin[i][r] = v[i][r];
-  } else {
-    if (t1 == T) {
-#pragma unroll
-      for (int i = 0; i < RT; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) st[T][i][r] = v[i][r];
-    } else {
-#pragma unroll
-      for (int i = 0; i < RT; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) v[i][r] = st[T][i][r] + v[i][r];
-      push_rec<T + 1, RT, LOGP>(t1, st, v, fin);
-    }
-  }
-}
+// Workgroup: 4 waves = RH row groups x CG = 4/RH column groups.  A wave owns
+// RT row tiles x CT column tiles over the workgroup's K range, which is NQ
+// whole quarters (split s of 4/NQ); quarters are summed in order with at most
+// two saved tiles.  Activations (fp16 integer fragments and block scales) are
+// staged per chunk of KC blocks (KC = 4, or 1 when a quarter is not a whole
+// number of 4-block groups) through a double-buffered LDS ring shared by the
+// 4 waves; weights and weight scales stream straight into registers one
+// chunk ahead.  With NQ < 4 the workgroups of one column block write 4/NQ
+// output slices that the consumer combines as (s0+s1) or ((s0+s1)+(s2+s3)).
+constexpr int QG_WRT = 8;  // most row tiles per workgroup (128 rows)
 
-template <int RT, int LOGP>
-__device__ __forceinline__ void push_leaf_dyn(int leaf, float (&st)[LOGP][RT][4], float (&v)[RT][4],
-                                              float (&fin)[RT][4]) {
-  push_rec<0, RT, LOGP>(__builtin_ctz(~(unsigned)leaf), st, v, fin);
-}
-
-constexpr int QG_MT = 8;   // row tiles staged per workgroup (128 rows)
-
-template <int RT, int RH, int BITS, int LOGP>
+template <int RT, int RH, int CT, int BITS, int NQ, int KC>
 __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W,
                                                   const uint16_t* __restrict__ Ws,
                                                   const _Float16* __restrict__ X,
-                                                  const float* __restrict__ Xs, int nb, int mpad,
-                                                  float* __restrict__ Y, int ldy, int m_rows,
-                                                  size_t slice_stride) {
-  constexpr int CTW = 4 / RH;
+                                                  const float* __restrict__ Xs, int nb, int nct,
+                                                  int mpad, float* __restrict__ Y, int ldy,
+                                                  int m_rows, size_t slice_stride) {
+  constexpr int CG = 4 / RH;
+  constexpr int WRT = RH * RT;
   constexpr int DW = BITS == 4 ? 1 : 2;
-  constexpr int PPW = 1 << LOGP;
-  __shared__ u32x4 s_act[2][QG_MT * 4 * 64];     // [buf][rt][bb][64 x 16B]
-  __shared__ float s_xs[2][4][QG_MT * 16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int APT = (WRT * KC * 64 + 255) / 256;  // 16-byte act pieces per thread per chunk
+  constexpr int XPT = (WRT * KC * 16 + 255) / 256;  // activation scales per thread per chunk
+  __shared__ u32x4 s_act[2][WRT * KC * 64];         // [buf][rt][kc][64 lanes x 16 B]
+  __shared__ float s_xs[2][KC][WRT * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nn = lane & 15, g = lane >> 4;
-  const int ctw = wave % CTW, rh = wave / CTW;
-  const int ct = blockIdx.x * CTW + ctw;
-  const int q = blockIdx.y;
-  const int rg = blockIdx.z;                       // group of QG_MT row tiles
-  const int mt_all = mpad >> 4;
-  const int mt = min(QG_MT, mt_all - rg * QG_MT);  // row tiles in this group
-  const int nb4 = nb >> 2;
-  const int c = (nb + 63) >> 6;
-  const int p0 = q * PPW;
-  const int b_begin = min(nb, p0 * c), b_end = min(nb, (p0 + PPW) * c);
-  const int nchunk = (b_end - b_begin) >> 2;
-  const uint32_t* Wt = W + (size_t)ct * nb4 * 256 * DW;
-  const uint16_t* St = Ws + (size_t)ct * nb4 * 64;
-  const u32x4* Xg = reinterpret_cast<const u32x4*>(X) + (size_t)rg * QG_MT * nb * 64;
-  const int pieces = mt * 256;                     // 16-byte act pieces per chunk
-  const int row0 = rg * QG_MT * 16;
-
-  float st[LOGP][RT][4];
-  float acc[RT][4], fin[RT][4];
+  const int cg = wave % CG, rh = wave / CG;
+  const int ct0 = (blockIdx.x * CG + cg) * CT;
+  const int split = blockIdx.y;
+  const int rg = blockIdx.z;
+  const int mt = min(WRT, (mpad >> 4) - rg * WRT);  // row tiles in this group
+  const int nb4 = nb >> 2, qs = nb >> 2;
+  const int b_begin = split * NQ * qs;
+  const int cpq = qs / KC;                          // chunks per quarter
+  const int nchunk = NQ * cpq;
+  const int row0 = rg * WRT * 16;
+  const u32x4* Xg = reinterpret_cast<const u32x4*>(X) + (size_t)rg * WRT * nb * 64;
+  int ctl[CT];
 #pragma unroll
-  for (int i = 0; i < RT; i++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) { acc[i][r] = 0.0f; fin[i][r] = 0.0f; }
+  for (int c = 0; c < CT; c++) ctl[c] = min(ct0 + c, nct - 1);  // clamped for loads
 
-  // register staging for the next chunk (macros, so every array index is a
-  // compile-time constant and stays in registers)
-  u32x4 pa[QG_MT];
-  float pxs[2];
-  u32x4 pw[DW];
-  u32x2 psc;
-#define QG_LOAD_CHUNK(CH)                                                                        \
-  do {                                                                                           \
-    const int b0_ = b_begin + 4 * (CH), bq_ = b0_ >> 2;                                          \
-    _Pragma("unroll") for (int k = 0; k < QG_MT; k++) {                                          \
-      const int piece = min(tid + 256 * k, pieces - 1);                                          \
-      pa[k] = Xg[((size_t)(piece >> 8) * nb + b0_) * 64 + (piece & 255)];                         \
-    }                                                                                            \
-    _Pragma("unroll") for (int k = 0; k < 2; k++) {                                              \
-      const int e = tid + 256 * k;                                                               \
-      const int rr = e & 127;                                                                    \
-      const float v_ = Xs[(size_t)(b0_ + (e >> 7)) * mpad + row0 + min(rr, mt * 16 - 1)];         \
-      pxs[k] = (rr < mt * 16) ? v_ : 0.0f;                                                       \
-    }                                                                                            \
-    const u32x4* wp_ = reinterpret_cast<const u32x4*>(Wt + ((size_t)bq_ * 256 + (g * 16 + nn) * 4) * DW); \
-    _Pragma("unroll") for (int k = 0; k < DW; k++) pw[k] = wp_[k];                               \
-    psc = *reinterpret_cast<const u32x2*>(St + ((size_t)bq_ * 16 + nn) * 4);                     \
+  float acc[RT][CT][4];
+  float sv0[(NQ > 1) ? RT : 1][CT][4];
+  float sv1[(NQ > 2) ? RT : 1][CT][4];
+
+  u32x4 pa[APT];
+  float pxs[XPT];
+  uint32_t pw[CT][KC * DW];
+  uint32_t psc[CT][KC * 2];
+#define QG_LOAD_CHUNK(CH)                                                                          \
+  do {                                                                                             \
+    const int b_ = b_begin + (CH) * KC;                                                            \
+    _Pragma("unroll") for (int k = 0; k < APT; k++) {                                              \
+      const int e = tid + 256 * k;                                                                 \
+      const int rt_ = min(e / (KC * 64), mt - 1);                                                  \
+      pa[k] = Xg[((size_t)rt_ * nb + b_) * 64 + e % (KC * 64)];                                    \
+    }                                                                                              \
+    _Pragma("unroll") for (int k = 0; k < XPT; k++) {                                              \
+      const int e = tid + 256 * k;                                                                 \
+      const int rr = e % (WRT * 16), kc_ = min(e / (WRT * 16), KC - 1);                            \
+      const float v_ = Xs[(size_t)(b_ + kc_) * mpad + row0 + min(rr, mt * 16 - 1)];               \
+      pxs[k] = (rr < mt * 16) ? v_ : 0.0f;                                                         \
+    }                                                                                              \
+    const int bq_ = b_ >> 2, bb_ = b_ & 3;                                                         \
+    _Pragma("unroll") for (int c = 0; c < CT; c++) {                                               \
+      const uint32_t* wp_ = W + ((size_t)ctl[c] * nb4 + bq_) * 256 * DW + (g * 16 + nn) * 4 * DW;   \
+      const uint32_t* sp_ = reinterpret_cast<const uint32_t*>(                                     \
+          Ws + (((size_t)ctl[c] * nb4 + bq_) * 4 + g) * 16);                                       \
+      if constexpr (KC == 4) {                                                                     \
+        const u32x4 w0_ = *reinterpret_cast<const u32x4*>(wp_);                                    \
+        _Pragma("unroll") for (int k = 0; k < 4; k++) pw[c][k] = w0_[k];                           \
+        if constexpr (DW == 2) {                                                                   \
+          const u32x4 w1_ = *reinterpret_cast<const u32x4*>(wp_ + 4);                              \
+          _Pragma("unroll") for (int k = 0; k < 4; k++) pw[c][4 + k] = w1_[k];                     \
+        }                                                                                          \
+        const u32x4 s0_ = *reinterpret_cast<const u32x4*>(sp_);                                    \
+        const u32x4 s1_ = *reinterpret_cast<const u32x4*>(sp_ + 4);                                \
+        _Pragma("unroll") for (int k = 0; k < 4; k++) { psc[c][k] = s0_[k]; psc[c][4 + k] = s1_[k]; } \
+      } else {                                                                                     \
+        if constexpr (DW == 1) pw[c][0] = wp_[bb_];                                                \
+        else {                                                                                     \
+          const u32x2 w_ = *reinterpret_cast<const u32x2*>(wp_ + 2 * bb_);                         \
+          pw[c][0] = w_[0];                                                                        \
+          pw[c][1] = w_[1];                                                                        \
+        }                                                                                          \
+        const u32x2 s_ = *reinterpret_cast<const u32x2*>(sp_ + 2 * bb_);                           \
+        psc[c][0] = s_[0];                                                                         \
+        psc[c][1] = s_[1];                                                                         \
+      }                                                                                            \
+    }                                                                                              \
   } while (0)
-#define QG_STORE_CHUNK(BUF)                                                                      \
-  do {                                                                                           \
-    _Pragma("unroll") for (int k = 0; k < QG_MT; k++) s_act[(BUF)][tid + 256 * k] = pa[k];       \
-    _Pragma("unroll") for (int k = 0; k < 2; k++) {                                              \
-      const int e = tid + 256 * k;                                                               \
-      s_xs[(BUF)][e >> 7][e & 127] = pxs[k];                                                     \
-    }                                                                                            \
+#define QG_STORE_CHUNK(BUF)                                                                        \
+  do {                                                                                             \
+    _Pragma("unroll") for (int k = 0; k < APT; k++) {                                              \
+      const int e = tid + 256 * k;                                                                 \
+      if (APT * 256 == WRT * KC * 64 || e < WRT * KC * 64) s_act[(BUF)][e] = pa[k];                \
+    }                                                                                              \
+    _Pragma("unroll") for (int k = 0; k < XPT; k++) {                                              \
+      const int e = tid + 256 * k;                                                                 \
+      if (XPT * 256 == WRT * KC * 16 || e < WRT * KC * 16)                                         \
+        s_xs[(BUF)][e / (WRT * 16)][e % (WRT * 16)] = pxs[k];                  \
+    }                                                                                              \
   } while (0)
 
-  int leaf = 0;  // next leaf (part) index relative to p0
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (nchunk > 0) {
-    QG_LOAD_CHUNK(0);
-    QG_STORE_CHUNK(0);
-  }
+  QG_LOAD_CHUNK(0);
+  QG_STORE_CHUNK(0);
   __syncthreads();
-  for (int ch = 0; ch < nchunk; ch++) {
-    const int buf = ch & 1;
-    u32x4 cw[DW];
-#pragma unroll
-    for (int k = 0; k < DW; k++) cw[k] = pw[k];
-    const u32x2 csc = psc;
-    if (ch + 1 < nchunk) QG_LOAD_CHUNK(ch + 1);
-    const int b0 = b_begin + 4 * ch;
-#pragma unroll
-    for (int bb = 0; bb < 4; bb++) {
-      h8 wv;
-      if (BITS == 4) {
-        const uint32_t x = bb == 0 ? cw[0][0] : bb == 1 ? cw[0][1] : bb == 2 ? cw[0][2] : cw[0][3];
-        wv = unpack_q4(x);
-      } else {
-        const u32x4 lo = cw[bb >> 1];
-        const uint32_t x0 = (bb & 1) ? lo[2] : lo[0], x1 = (bb & 1) ? lo[3] : lo[1];
-        wv = unpack_q8(x0, x1);
-      }
-      const uint32_t sh = (bb < 2) ? csc[0] : csc[1];
-      const float dw = h2f_bits((uint16_t)((bb & 1) ? (sh >> 16) : (sh & 0xFFFFu)));
-#pragma unroll
-      for (int i = 0; i < RT; i++) {
-        const int rt = rh * RT + i;
-        if (rt < mt) {
-          const u32x4 a4 = s_act[buf][(rt * 4 + bb) * 64 + g * 16 + nn];
-          const h8 av = __builtin_bit_cast(h8, a4);
-          const f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, wv, zero, 0, 0, 0);
-          const f4 xs = *reinterpret_cast<const f4*>(&s_xs[buf][bb][rt * 16 + g * 4]);
-#pragma unroll
-          for (int r = 0; r < 4; r++) acc[i][r] = __builtin_fmaf(d[r], dw * xs[r], acc[i][r]);
-        }
-      }
-      const int b = b0 + bb;
-      if ((b + 1) % c == 0 || b + 1 == nb) {
-        push_leaf_dyn<RT, LOGP>(leaf, st, acc, fin);
-        leaf++;
-#pragma unroll
-        for (int i = 0; i < RT; i++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) acc[i][r] = 0.0f;
-      }
-    }
-    if (ch + 1 < nchunk) QG_STORE_CHUNK(buf ^ 1);
-    __syncthreads();
-  }
-#undef QG_LOAD_CHUNK
-#undef QG_STORE_CHUNK
-  // empty trailing parts of the subtree
-  for (; leaf < PPW; leaf++) {
+  int ch = 0;
+  for (int kq = 0; kq < NQ; kq++) {
 #pragma unroll
     for (int i = 0; i < RT; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[i][r] = 0.0f;
-    push_leaf_dyn<RT, LOGP>(leaf, st, acc, fin);
+      for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][c][r] = 0.0f;
+    for (int cc = 0; cc < cpq; cc++, ch++) {
+      const int buf = ch & 1;
+      uint32_t cw[CT][KC * DW], csc[CT][KC * 2];
+#pragma unroll
+      for (int c = 0; c < CT; c++) {
+#pragma unroll
+        for (int k = 0; k < KC * DW; k++) cw[c][k] = pw[c][k];
+#pragma unroll
+        for (int k = 0; k < KC * 2; k++) csc[c][k] = psc[c][k];
+      }
+      // The last chunk reloads itself, so every iteration is one straight-line
+      // block (the ring slot it refills is no longer read by any wave).
+      QG_LOAD_CHUNK(min(ch + 1, nchunk - 1));
+#pragma unroll
+      for (int kc = 0; kc < KC; kc++) {
+        h8 wv[CT];
+        float dw[CT][4];
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+          if constexpr (BITS == 4) wv[c] = unpack_q4(cw[c][kc]);
+          else wv[c] = unpack_q8(cw[c][2 * kc], cw[c][2 * kc + 1]);
+          const uint32_t s01 = csc[c][2 * kc], s23 = csc[c][2 * kc + 1];
+          dw[c][0] = h2f_bits((uint16_t)(s01 & 0xFFFFu));
+          dw[c][1] = h2f_bits((uint16_t)(s01 >> 16));
+          dw[c][2] = h2f_bits((uint16_t)(s23 & 0xFFFFu));
+          dw[c][3] = h2f_bits((uint16_t)(s23 >> 16));
+        }
+        // Row tiles past mt compute on stale LDS and are never stored, which
+        // keeps the hot loop free of branches.
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+          const int rt = rh * RT + i;
+          const h8 av = __builtin_bit_cast(h8, s_act[buf][(rt * KC + kc) * 64 + g * 16 + nn]);
+          const float dx = s_xs[buf][kc][rt * 16 + nn];
+#pragma unroll
+          for (int c = 0; c < CT; c++) {
+            const f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[c], av, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              acc[i][c][r] = __builtin_fmaf(d[r], dw[c][r] * dx, acc[i][c][r]);
+          }
+        }
+      }
+      // interleave: one MFMA, then a run of VALU work of the previous tiles
+#pragma unroll
+      for (int k = 0; k < KC * RT * CT; k++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+      }
+      QG_STORE_CHUNK(buf ^ 1);
+      __syncthreads();
+    }
+    // quarter kq complete: (q0 + q1) is kept in sv0, q2 in sv1; the last
+    // quarter stays in acc
+    if constexpr (NQ == 2) {
+      if (kq == 0) {
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+          for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv0[i][c][r] = acc[i][c][r];
+      }
+    } else if constexpr (NQ == 4) {
+      if (kq == 0) {
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+          for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv0[i][c][r] = acc[i][c][r];
+      } else if (kq == 1) {
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+          for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv0[i][c][r] = sv0[i][c][r] + acc[i][c][r];
+      } else if (kq == 2) {
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+          for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv1[i][c][r] = acc[i][c][r];
+      }
+    }
   }
-  float* Yq = Y + (size_t)q * slice_stride;
-  const int col = ct * 16 + nn;
+#undef QG_LOAD_CHUNK
+#undef QG_STORE_CHUNK
+  float* Yq = Y + (size_t)split * slice_stride;
 #pragma unroll
   for (int i = 0; i < RT; i++) {
     const int rt = rh * RT + i;
+    const int m = row0 + rt * 16 + nn;
+    if (rt >= mt || m >= m_rows) continue;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int m = row0 + rt * 16 + g * 4 + r;
-      if (rt < mt && m < m_rows) Yq[(size_t)m * ldy + col] = fin[i][r];
+    for (int c = 0; c < CT; c++) {
+      if (ct0 + c >= nct) continue;
+      f4 o;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if constexpr (NQ == 1) o[r] = acc[i][c][r];
+        else if constexpr (NQ == 2) o[r] = sv0[i][c][r] + acc[i][c][r];
+        else o[r] = sv0[i][c][r] + (sv1[i][c][r] + acc[i][c][r]);
+      }
+      *reinterpret_cast<f4*>(Yq + (size_t)m * ldy + (ct0 + c) * 16 + 4 * g) = o;
     }
   }
 }
 
-int qgemm_splits(int n, int mpad) {
-  const int mt = mpad / 16;
-  const int rh = mt > 4 ? 2 : 1;
-  const int ctw = 4 / rh;
-  const int wgs = (n / 16 + ctw - 1) / ctw * ((mt + QG_MT - 1) / QG_MT);
-  if (wgs >= 512) return 1;
-  if (wgs * 2 >= 512) return 2;
-  return 4;
+namespace {
+struct QgPlan {
+  int rt, rh, ct, splits;
+};
+// Row tiling from the padded batch; then the widest column block and fewest
+// K splits that still give >= 384 workgroups (1.5 per CU) on 256 CUs.  Q8 at
+// 128 rows keeps one column tile per wave (two exceed the register file).
+QgPlan qg_plan(int n, int mpad, int bits) {
+  const int mt_all = mpad / 16;
+  const int wrt = mt_all < QG_WRT ? mt_all : QG_WRT;
+  QgPlan p{};
+  p.rh = wrt > 4 ? 2 : 1;
+  p.rt = p.rh == 2 ? 4 : (wrt > 2 ? 4 : (wrt > 1 ? 2 : 1));
+  const int cg = 4 / p.rh;
+  const int groups = (mt_all + p.rh * p.rt - 1) / (p.rh * p.rt);
+  const int nct = n / 16;
+  for (int ct = (bits == 8 && p.rh == 2) ? 1 : 2; ct >= 1; ct--)
+    for (int s = 1; s <= 4; s *= 2) {
+      const int wgs = (nct + cg * ct - 1) / (cg * ct) * s * groups;
+      if (wgs >= 384) { p.ct = ct; p.splits = s; return p; }
+    }
+  p.ct = 1;
+  p.splits = 4;
+  return p;
 }
+}  // namespace
+
+int qgemm_splits(int n, int mpad, int bits) { return qg_plan(n, mpad, bits).splits; }
 
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride) {
   const int nb = w.k / 32;
+  if (w.n % 16 || nb % 4 || splits < 1) return hipErrorInvalidValue;
+  QgPlan p = qg_plan(w.n, x.mpad, w.bits);
+  if (splits != p.splits) {
+    if (splits != 1 && splits != 2 && splits != 4) return hipErrorInvalidValue;
+    p.splits = splits;
+  }
+  const int nct = w.n / 16;
+  const int cg = 4 / p.rh;
   const int mt_all = x.mpad / 16;
-  const int mt = mt_all < QG_MT ? mt_all : QG_MT;
-  const int rh = mt > 4 ? 2 : 1;
-  const int rt = rh == 2 ? 4 : (mt > 2 ? 4 : (mt > 1 ? 2 : 1));
-  const int ctw = 4 / rh;
-  if ((w.n / 16) % ctw) return hipErrorInvalidValue;
-  dim3 grid(w.n / 16 / ctw, splits, (mt_all + QG_MT - 1) / QG_MT);
+  dim3 grid((nct + cg * p.ct - 1) / (cg * p.ct), p.splits, (mt_all + p.rh * p.rt - 1) / (p.rh * p.rt));
   const uint32_t* W = (const uint32_t*)w.w;
-#define RSTR_QG(R, H, B, LP)                                                                       \
-  hipLaunchKernelGGL((k_qgemm<R, H, B, LP>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
-                     ldy, m_rows, slice_stride)
-#define RSTR_QG_S(R, H, B)                                 \
-  do {                                                     \
-    if (splits == 1) RSTR_QG(R, H, B, 6);                  \
-    else if (splits == 2) RSTR_QG(R, H, B, 5);             \
-    else RSTR_QG(R, H, B, 4);                              \
+  const bool aligned = (nb / 4) % 4 == 0;  // quarters are whole 4-block chunks
+#define RSTR_QG(R, H, C, B, Q)                                                                      \
+  do {                                                                                              \
+    if (aligned)                                                                                    \
+      hipLaunchKernelGGL((k_qgemm<R, H, C, B, Q, 4>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb,  \
+                         nct, x.mpad, y, ldy, m_rows, slice_stride);                                \
+    else                                                                                            \
+      hipLaunchKernelGGL((k_qgemm<R, H, C, B, Q, 1>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb,  \
+                         nct, x.mpad, y, ldy, m_rows, slice_stride);                                \
   } while (0)
-#define RSTR_QG_R(B)                                       \
-  do {                                                     \
-    if (rh == 2) RSTR_QG_S(4, 2, B);                       \
-    else if (rt == 4) RSTR_QG_S(4, 1, B);                  \
-    else if (rt == 2) RSTR_QG_S(2, 1, B);                  \
-    else RSTR_QG_S(1, 1, B);                               \
+#define RSTR_QG_S(R, H, C, B)                               \
+  do {                                                      \
+    if (p.splits == 1) RSTR_QG(R, H, C, B, 4);              \
+    else if (p.splits == 2) RSTR_QG(R, H, C, B, 2);         \
+    else RSTR_QG(R, H, C, B, 1);                            \
   } while (0)
-  if (splits != 1 && splits != 2 && splits != 4) return hipErrorInvalidValue;
+#define RSTR_QG_C(R, H, B)                                  \
+  do {                                                      \
+    if (p.ct == 2) RSTR_QG_S(R, H, 2, B);                   \
+    else RSTR_QG_S(R, H, 1, B);                             \
+  } while (0)
+#define RSTR_QG_R(B)                                        \
+  do {                                                      \
+    if (p.rh == 2) RSTR_QG_C(4, 2, B);                      \
+    else if (p.rt == 4) RSTR_QG_C(4, 1, B);                 \
+    else if (p.rt == 2) RSTR_QG_C(2, 1, B);                 \
+    else RSTR_QG_C(1, 1, B);                                \
+  } while (0)
   if (w.bits == 4) RSTR_QG_R(4);
   else RSTR_QG_R(8);
 #undef RSTR_QG_R
+#undef RSTR_QG_C
 #undef RSTR_QG_S
 #undef RSTR_QG
   return hipGetLastError();
@@ -422,20 +497,25 @@ __device__ __forceinline__ f4 sl_load4(const Slices& s, size_t i) {
 }
 
 // ===========================================================================
-// Row kernels: one wavefront per row.  Canonical sum of squares: lane l owns
-// float4 chunks c = l + 64i (elements 4c..4c+3), accumulates fmaf(x,x,acc) in
-// element order, lanes combine by the pairwise tree.
+// Row kernels: one 256-thread workgroup per row.  Canonical sum of squares:
+// thread t owns float4 chunks c = t + 256i (elements 4c..4c+3, i.e. slot
+// (element/4) mod 256), accumulates fmaf(x,x,acc) in element order; the 256
+// slots combine by the pairwise tree (xor butterfly inside each wave, then
+// ((w0+w1)+(w2+w3)) across the four waves).
 // ===========================================================================
-__device__ __forceinline__ float row_sumsq(const float* __restrict__ x, int n4, int lane) {
-  float acc = 0.0f;
-  for (int c = lane; c < n4; c += 64) {
-    f4 v = *reinterpret_cast<const f4*>(x + 4 * c);
-    acc = __builtin_fmaf(v[0], v[0], acc);
-    acc = __builtin_fmaf(v[1], v[1], acc);
-    acc = __builtin_fmaf(v[2], v[2], acc);
-    acc = __builtin_fmaf(v[3], v[3], acc);
-  }
-  return wave_tree_sum(acc);
+__device__ __forceinline__ float block_tree_sum(float v, float* sh4) {
+  v = wave_tree_sum(v);
+  __syncthreads();  // sh4 may still be read by an earlier reduction
+  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (sh4[0] + sh4[1]) + (sh4[2] + sh4[3]);
+}
+
+__device__ __forceinline__ float fma4_sq(f4 v, float acc) {
+  acc = __builtin_fmaf(v[0], v[0], acc);
+  acc = __builtin_fmaf(v[1], v[1], acc);
+  acc = __builtin_fmaf(v[2], v[2], acc);
+  return __builtin_fmaf(v[3], v[3], acc);
 }
 
 __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
@@ -469,21 +549,22 @@ __device__ __forceinline__ void quant_store(f4 y, bool valid, int c, int row, in
 
 __global__ __launch_bounds__(256) void k_rms_quant(const float* __restrict__ x,
                                                    const float* __restrict__ g, float goff, float eps,
-                                                   int rows, int n, _Float16* __restrict__ Q,
+                                                   int n, _Float16* __restrict__ Q,
                                                    float* __restrict__ S, int mpad) {
-  int lane = threadIdx.x & 63;
-  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  __shared__ float sh4[4];
+  const int tid = threadIdx.x, row = blockIdx.x;
   const float* xr = x + (size_t)row * n;
-  int n4 = n >> 2, nb = n >> 5;
-  float r = rms_scale(row_sumsq(xr, n4, lane), n, eps);
-  for (int c0 = 0; c0 < n4; c0 += 64) {
-    int c = c0 + lane;
-    bool valid = c < n4;
+  const int n4 = n >> 2, nb = n >> 5;
+  float acc = 0.0f;
+  for (int c = tid; c < n4; c += 256) acc = fma4_sq(*reinterpret_cast<const f4*>(xr + 4 * c), acc);
+  const float r = rms_scale(block_tree_sum(acc, sh4), n, eps);
+  for (int c0 = 0; c0 < n4; c0 += 256) {
+    const int c = c0 + tid;
+    const bool valid = c < n4;
     f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
     if (valid) {
-      f4 v = *reinterpret_cast<const f4*>(xr + 4 * c);
-      f4 gg = *reinterpret_cast<const f4*>(g + 4 * c);
+      const f4 v = *reinterpret_cast<const f4*>(xr + 4 * c);
+      const f4 gg = *reinterpret_cast<const f4*>(g + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; i++) y[i] = (v[i] * r) * (goff + gg[i]);
     }
@@ -493,8 +574,9 @@ __global__ __launch_bounds__(256) void k_rms_quant(const float* __restrict__ x,
 
 hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,
                             int rows, int n, ActBuf& out) {
-  hipLaunchKernelGGL(k_rms_quant, dim3((rows + 3) / 4), dim3(256), 0, st, x, g, goff, eps, rows, n,
-                     out.q, out.s, out.mpad);
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rms_quant, dim3(rows), dim3(256), 0, st, x, g, goff, eps, n, out.q, out.s,
+                     out.mpad);
   return hipGetLastError();
 }
 
@@ -504,52 +586,43 @@ hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, floa
 // followed by the next layer's input norm (or the final norm of the head).
 __global__ __launch_bounds__(256) void k_residual_norm_quant(
     Slices o, const float* __restrict__ x, float* __restrict__ xout,
-    const float* __restrict__ post, const float* __restrict__ gnext, float goff, float eps, int rows,
-    int n, _Float16* __restrict__ Q, float* __restrict__ S, int mpad) {
-  int lane = threadIdx.x & 63;
-  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  int n4 = n >> 2, nb = n >> 5;
+    const float* __restrict__ post, const float* __restrict__ gnext, float goff, float eps, int n,
+    _Float16* __restrict__ Q, float* __restrict__ S, int mpad) {
+  __shared__ float sh4[4];
+  const int tid = threadIdx.x, row = blockIdx.x;
+  const int n4 = n >> 2, nb = n >> 5;
   const size_t orow = (size_t)row * n;
-  const float* xr = x + (size_t)row * n;
-  float* xo = xout + (size_t)row * n;
+  const float* xr = x + orow;
+  float* xo = xout + orow;
   float r1 = 1.0f;
   if (post) {
     float a = 0.0f;
-    for (int c = lane; c < n4; c += 64) {
-      f4 v = sl_load4(o, orow + 4 * c);
-      a = __builtin_fmaf(v[0], v[0], a);
-      a = __builtin_fmaf(v[1], v[1], a);
-      a = __builtin_fmaf(v[2], v[2], a);
-      a = __builtin_fmaf(v[3], v[3], a);
-    }
-    r1 = rms_scale(wave_tree_sum(a), n, eps);
+    for (int c = tid; c < n4; c += 256) a = fma4_sq(sl_load4(o, orow + 4 * c), a);
+    r1 = rms_scale(block_tree_sum(a, sh4), n, eps);
   }
   float acc = 0.0f;
-  for (int c = lane; c < n4; c += 64) {
+  for (int c = tid; c < n4; c += 256) {
     f4 ov = sl_load4(o, orow + 4 * c);
-    f4 xv = *reinterpret_cast<const f4*>(xr + 4 * c);
+    const f4 xv = *reinterpret_cast<const f4*>(xr + 4 * c);
     if (post) {
-      f4 pg = *reinterpret_cast<const f4*>(post + 4 * c);
+      const f4 pg = *reinterpret_cast<const f4*>(post + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; i++) ov[i] = (ov[i] * r1) * (goff + pg[i]);
     }
     f4 xm;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      xm[i] = xv[i] + ov[i];
-      acc = __builtin_fmaf(xm[i], xm[i], acc);
-    }
+    for (int i = 0; i < 4; i++) xm[i] = xv[i] + ov[i];
+    acc = fma4_sq(xm, acc);
     *reinterpret_cast<f4*>(xo + 4 * c) = xm;
   }
-  float r2 = rms_scale(wave_tree_sum(acc), n, eps);
-  for (int c0 = 0; c0 < n4; c0 += 64) {
-    int c = c0 + lane;
-    bool valid = c < n4;
+  const float r2 = rms_scale(block_tree_sum(acc, sh4), n, eps);
+  for (int c0 = 0; c0 < n4; c0 += 256) {
+    const int c = c0 + tid;
+    const bool valid = c < n4;
     f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
     if (valid) {
-      f4 v = *reinterpret_cast<const f4*>(xo + 4 * c);
-      f4 gg = *reinterpret_cast<const f4*>(gnext + 4 * c);
+      const f4 v = *reinterpret_cast<const f4*>(xo + 4 * c);  // written by this thread above
+      const f4 gg = *reinterpret_cast<const f4*>(gnext + 4 * c);
 #pragma unroll
       for (int i = 0; i < 4; i++) y[i] = (v[i] * r2) * (goff + gg[i]);
     }
@@ -560,46 +633,46 @@ __global__ __launch_bounds__(256) void k_residual_norm_quant(
 hipError_t launch_post_attn(hipStream_t st, Slices o, const float* x, float* xmid,
                             const float* paln, const float* pfln, float goff, float eps, int rows,
                             int n, ActBuf& out) {
-  hipLaunchKernelGGL(k_residual_norm_quant, dim3((rows + 3) / 4), dim3(256), 0, st, o, x, xmid, paln,
-                     pfln, goff, eps, rows, n, out.q, out.s, out.mpad);
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_residual_norm_quant, dim3(rows), dim3(256), 0, st, o, x, xmid, paln, pfln, goff,
+                     eps, n, out.q, out.s, out.mpad);
   return hipGetLastError();
 }
 
 hipError_t launch_post_ffn(hipStream_t st, Slices dn, const float* xmid, float* xout,
                            const float* pffln, const float* gnext, float goff, float eps, int rows,
                            int n, ActBuf& out) {
-  hipLaunchKernelGGL(k_residual_norm_quant, dim3((rows + 3) / 4), dim3(256), 0, st, dn, xmid, xout,
-                     pffln, gnext, goff, eps, rows, n, out.q, out.s, out.mpad);
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_residual_norm_quant, dim3(rows), dim3(256), 0, st, dn, xmid, xout, pffln, gnext,
+                     goff, eps, n, out.q, out.s, out.mpad);
   return hipGetLastError();
 }
 
 // hh = act(gate) * up (gelu-mul! / silu-mul!), quantised for the down projection.
-__global__ __launch_bounds__(256) void k_act_quant(Slices gu, int rows, int ff,
-                                                   int geglu, _Float16* __restrict__ Q,
+// Element-wise with per-block quantisation: workgroups tile (row, 1024 columns).
+__global__ __launch_bounds__(256) void k_act_quant(Slices gu, int ff, int geglu,
+                                                   _Float16* __restrict__ Q,
                                                    float* __restrict__ S, int mpad) {
-  int lane = threadIdx.x & 63;
-  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int row = blockIdx.y;
   const size_t gr = (size_t)row * 2 * ff;
-  int n4 = ff >> 2, nb = ff >> 5;
-  for (int c0 = 0; c0 < n4; c0 += 64) {
-    int c = c0 + lane;
-    bool valid = c < n4;
-    f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (valid) {
-      f4 gv = sl_load4(gu, gr + 4 * c);
-      f4 uv = sl_load4(gu, gr + ff + 4 * c);
+  const int n4 = ff >> 2, nb = ff >> 5;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const bool valid = c < n4;
+  f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (valid) {
+    const f4 gv = sl_load4(gu, gr + 4 * c);
+    const f4 uv = sl_load4(gu, gr + ff + 4 * c);
 #pragma unroll
-      for (int i = 0; i < 4; i++) y[i] = (geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
-    }
-    quant_store(y, valid, c, row, nb, mpad, Q, S);
+    for (int i = 0; i < 4; i++) y[i] = (geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
   }
+  quant_store(y, valid, c, row, nb, mpad, Q, S);
 }
 
 hipError_t launch_act_quant(hipStream_t st, Slices gu, int rows, int ff, int geglu,
                             ActBuf& out) {
-  hipLaunchKernelGGL(k_act_quant, dim3((rows + 3) / 4), dim3(256), 0, st, gu, rows, ff, geglu, out.q,
-                     out.s, out.mpad);
+  if (rows <= 0) return hipSuccess;
+  dim3 grid((ff / 4 + 255) / 256, rows);
+  hipLaunchKernelGGL(k_act_quant, grid, dim3(256), 0, st, gu, ff, geglu, out.q, out.s, out.mpad);
   return hipGetLastError();
 }
 
@@ -651,6 +724,8 @@ __global__ __launch_bounds__(64) void k_qkv_post(Slices y, int n_q, int n_kv,
       a = __builtin_fmaf(v[2], v[2], a);
       a = __builtin_fmaf(v[3], v[3], a);
     }
+    // head_dim/4 <= 64 chunks: lane l holds slot l alone, and the tree over
+    // 64 lanes equals the 256-slot tree (the other slots are +0).
     r = rms_scale(wave_tree_sum(a), hd, eps);
   }
   for (int c = lane; c < hd4; c += 64) {
@@ -736,19 +811,45 @@ hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* le
 // c = j + LPT*i whose slices are c mod 16; slices merge by the fixed tree
 // (bit 3, 2, 1, 0 of the slice index), the last levels across lanes.
 // Softmax: m = max, p = exp(s - m).  PV: lane group g (16 lanes) takes tokens
-// t = g mod 4 in order, lanes own contiguous dims; groups merge ((0+1)+(2+3)).
+// t = g mod 4 in order, each lane owns a fixed set of dims; groups merge
+// ((0+1)+(2+3)).
+//
+// Memory path: one wave per work item streams the item's K rows and then its
+// V rows in chunks of 16 tokens through a ring of RB LDS buffers, filled by
+// direct-to-LDS loads (global_load_lds_dwordx4) issued RB-1 chunks ahead, so
+// a wave keeps up to (RB-1) * 16 rows in flight without holding them in
+// registers.  A 16-byte piece p of token row r lands at LDS slot
+// r*NP + (p ^ swz(r)); the swizzle makes both the QK reads (LPT lanes per
+// row) and the PV reads (16 lanes per row) hit 16 distinct bank groups.
+template <int HD, int LPT>
+__device__ __forceinline__ int attn_swz(int r) {
+  constexpr int NP = HD / 8;
+  if constexpr (NP >= 16) return (r % (16 / LPT)) * LPT;
+  else return ((r >> 1) & 1) * 4;  // HD = 64, LPT = 4
+}
+
+#define RSTR_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
 template <int HD, int G, int LPT>
 __global__ __launch_bounds__(64) void k_attn_split(
     int batch, int n_kv, int page_size, int pps, int split, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ lengths,
-    const int32_t* __restrict__ tab, float* __restrict__ part) {
-  constexpr int NCH = HD / 8;            // 8-dim chunks per head
-  constexpr int NCL = NCH / LPT;         // chunks per lane
-  constexpr int NSL = 16 / LPT;          // slice slots per lane (LPT <= 16)
-  constexpr int TPR = 64 / LPT;          // tokens per QK round
+    const int32_t* __restrict__ tab, float* __restrict__ part, int pg_cap) {
+  constexpr int NP = HD / 8;             // 16-byte pieces per row
+  constexpr int CT = 16;                 // tokens per chunk
+  constexpr int CU16 = CT * NP;          // 16-byte units per chunk
+  constexpr int LPC = CU16 / 64;         // DMA instructions per chunk
+  constexpr int RB = 4;                  // ring buffers
+  constexpr int NCL = NP / LPT;          // QK pieces per lane
+  constexpr int NSL = 16 / LPT;          // slice slots per lane
+  constexpr int TPP = 64 / LPT;          // tokens per QK pass
+  constexpr int PPL = NP >= 16 ? NP / 16 : 1;   // PV pieces per lane (HD 64: half a piece)
   constexpr int DPL = HD / 16;           // PV dims per lane
-  extern __shared__ float sc[];          // [G][split]
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  u32x4* ring = reinterpret_cast<u32x4*>(smem);                        // [RB][CU16]
+  float* sc = reinterpret_cast<float*>(smem + RB * CU16 * 16);          // [G][split]
+  int32_t* s_pg = reinterpret_cast<int32_t*>(sc + G * split);          // [pg_cap]
   const int lane = threadIdx.x;
   const int32_t* lo_t = tab;
   const int32_t* k0_t = tab + batch;
@@ -757,11 +858,11 @@ __global__ __launch_bounds__(64) void k_attn_split(
   const int total = base[batch];
   const int kvr = n_kv * HD;
   const int ts = lane / LPT, j = lane % LPT;
+  const int grp = lane >> 4, e16 = lane & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    // lane b: base[b] <= item < base[b+1]
     int lo = 0, hi = batch;
     while (hi - lo > 1) {
-      int mid = (lo + hi) >> 1;
+      const int mid = (lo + hi) >> 1;
       if (base[mid] <= item) lo = mid; else hi = mid;
     }
     const int b = lo;
@@ -772,7 +873,35 @@ __global__ __launch_bounds__(64) void k_attn_split(
     const int len = lengths[b];
     const int t0 = max(lo_t[b], k * split);
     const int t1 = min(len, (k + 1) * split);
+    const int T0 = t0 & ~(CT - 1);
+    const int nch = (t1 - T0 + CT - 1) / CT;
+    const int pg0 = t0 / page_size;
+    const int npg = (t1 - 1) / page_size - pg0 + 1;
     const int32_t* pt = page_table + (size_t)b * pps;
+    for (int i = lane; i < npg; i += 64) s_pg[i] = pt[pg0 + i];
+    const uint16_t* kbase = kp + kvh * HD;
+    const uint16_t* vbase = vp + kvh * HD;
+    __builtin_amdgcn_s_waitcnt(0);  // page ids visible before the first DMA address uses them
+    __syncthreads();
+
+    // DMA of stream position s (s < nch: K chunk s, else V chunk s - nch)
+    auto issue = [&](int s) {
+      const bool isk = s < nch;
+      const int c = isk ? s : s - nch;
+      const uint16_t* src = isk ? kbase : vbase;
+      u32x4* dst = ring + (s % RB) * CU16;
+#pragma unroll
+      for (int u = 0; u < LPC; u++) {
+        const int pos = u * 64 + lane;
+        const int r = pos / NP;
+        const int piece = (pos % NP) ^ attn_swz<HD, LPT>(r);
+        const int t = min(max(T0 + c * CT + r, t0), t1 - 1);
+        const int page = s_pg[t / page_size - pg0];
+        const uint16_t* g = src + ((size_t)page * page_size + (t % page_size)) * kvr + piece * 8;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), RSTR_LDS_PTR(dst + u * 64), 16, 0, 0);
+      }
+    };
+
     // query slices for the G heads of this kv group
     float qv[G][NCL][8];
 #pragma unroll
@@ -781,8 +910,8 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #pragma unroll
       for (int i = 0; i < NCL; i++) {
         const int cch = j + LPT * i;
-        f4 a = *reinterpret_cast<const f4*>(qh + 8 * cch);
-        f4 bq = *reinterpret_cast<const f4*>(qh + 8 * cch + 4);
+        const f4 a = *reinterpret_cast<const f4*>(qh + 8 * cch);
+        const f4 bq = *reinterpret_cast<const f4*>(qh + 8 * cch + 4);
 #pragma unroll
         for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = bq[e]; }
       }
@@ -790,52 +919,6 @@ __global__ __launch_bounds__(64) void k_attn_split(
     float mx[G];
 #pragma unroll
     for (int h = 0; h < G; h++) mx[h] = -__builtin_inff();
-    for (int T = t0 - (t0 % TPR); T < t1; T += TPR) {
-      const int t = T + ts;
-      const bool valid = (t >= t0) && (t < t1);
-      float s[G][NSL];
-#pragma unroll
-      for (int h = 0; h < G; h++)
-#pragma unroll
-        for (int u = 0; u < NSL; u++) s[h][u] = 0.0f;
-      if (valid) {
-        const int page = pt[t / page_size];
-        const uint16_t* krow = kp + ((size_t)page * page_size + (t % page_size)) * kvr + kvh * HD;
-#pragma unroll
-        for (int i = 0; i < NCL; i++) {
-          const int cch = j + LPT * i;
-          const h8 kv = *reinterpret_cast<const h8*>(krow + 8 * cch);
-#pragma unroll
-          for (int h = 0; h < G; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-              s[h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[e], s[h][i % NSL]);
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < G; h++) {
-        float v;
-        if constexpr (LPT == 4) v = (s[h][0] + s[h][2]) + (s[h][1] + s[h][3]);
-        else if constexpr (LPT == 8) v = s[h][0] + s[h][1];
-        else v = s[h][0];
-#pragma unroll
-        for (int m = LPT / 2; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-        const float score = v * scale;
-        if (valid) {
-          if (j == 0) sc[h * split + (t - t0)] = score;
-          mx[h] = fmaxf(mx[h], score);
-        }
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < G; h++) mx[h] = wave_max(mx[h]);
-    __syncthreads();
-    const int nt = t1 - t0;
-    for (int i = lane; i < nt; i += 64)
-#pragma unroll
-      for (int h = 0; h < G; h++) sc[h * split + i] = dexp(sc[h * split + i] - mx[h]);
-    __syncthreads();
-    const int grp = lane >> 4, e16 = lane & 15;
     float o[G][DPL], l[G];
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -843,31 +926,106 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #pragma unroll
       for (int d = 0; d < DPL; d++) o[h][d] = 0.0f;
     }
-    for (int T = t0 & ~3; T < t1; T += 4) {
-      const int t = T + grp;
-      if (t >= t0 && t < t1) {
-        const int page = pt[t / page_size];
-        const uint16_t* vrow =
-            vp + ((size_t)page * page_size + (t % page_size)) * kvr + kvh * HD + e16 * DPL;
-        float vv[DPL];
-        if constexpr (DPL >= 8) {
+
+    const int npos = 2 * nch;
 #pragma unroll
-          for (int d8 = 0; d8 < DPL; d8 += 8) {
-            const h8 hv = *reinterpret_cast<const h8*>(vrow + d8);
+    for (int s = 0; s < RB - 1; s++)
+      if (s < npos) issue(s);
+    for (int s = 0; s < npos; s++) {
+      if (s + RB - 1 < npos) {
+        // the ring slot being refilled was last read at step s-1, whose LDS
+        // reads have all returned
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        issue(s + RB - 1);
+        // wait until the DMA of position s has landed: RB-1 chunks may remain
+        __builtin_amdgcn_s_waitcnt(((LPC * (RB - 1)) & 0xF) | (((LPC * (RB - 1)) >> 4) << 14) | 0x0F70);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      }
+      __asm__ __volatile__("" ::: "memory");
+      const u32x4* buf = ring + (s % RB) * CU16;
+      if (s < nch) {
+        // ---- QK over the 16 rows of this chunk --------------------------------
 #pragma unroll
-            for (int e = 0; e < 8; e++) vv[d8 + e] = (float)hv[e];
+        for (int pass = 0; pass < CT / TPP + (CT % TPP ? 1 : 0); pass++) {
+          const int r = pass * TPP + ts;
+          const int t = T0 + s * CT + r;
+          const bool valid = r < CT && t >= t0 && t < t1;
+          const int rr = r < CT ? r : CT - 1;
+          float sv[G][NSL];
+#pragma unroll
+          for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int u = 0; u < NSL; u++) sv[h][u] = 0.0f;
+#pragma unroll
+          for (int i = 0; i < NCL; i++) {
+            const int piece = j + LPT * i;
+            const h8 kv = __builtin_bit_cast(h8, buf[rr * NP + (piece ^ attn_swz<HD, LPT>(rr))]);
+#pragma unroll
+            for (int h = 0; h < G; h++)
+#pragma unroll
+              for (int e = 0; e < 8; e++)
+                sv[h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[e], sv[h][i % NSL]);
           }
-        } else {
-          const h4 hv = *reinterpret_cast<const h4*>(vrow);
 #pragma unroll
-          for (int e = 0; e < 4; e++) vv[e] = (float)hv[e];
+          for (int h = 0; h < G; h++) {
+            float v;
+            if constexpr (LPT == 4) v = (sv[h][0] + sv[h][2]) + (sv[h][1] + sv[h][3]);
+            else if constexpr (LPT == 8) v = sv[h][0] + sv[h][1];
+            else v = sv[h][0];
+#pragma unroll
+            for (int m = LPT / 2; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+            const float score = v * scale;
+            if (valid) {
+              if (j == 0) sc[h * split + (t - t0)] = score;
+              mx[h] = fmaxf(mx[h], score);
+            }
+          }
         }
+        if (s == nch - 1) {
+          // ---- softmax numerators over the whole split ----------------------------
 #pragma unroll
-        for (int h = 0; h < G; h++) {
-          const float p = sc[h * split + (t - t0)];
-          l[h] = l[h] + p;
+          for (int h = 0; h < G; h++) mx[h] = wave_max(mx[h]);
+          __syncthreads();
+          const int nt = t1 - t0;
+          for (int i = lane; i < nt; i += 64)
 #pragma unroll
-          for (int d = 0; d < DPL; d++) o[h][d] = __builtin_fmaf(p, vv[d], o[h][d]);
+            for (int h = 0; h < G; h++) sc[h * split + i] = dexp(sc[h * split + i] - mx[h]);
+          __syncthreads();
+        }
+      } else {
+        // ---- PV over the 16 rows of this chunk: 4 rounds of one row per group ----
+        const int c = s - nch;
+#pragma unroll
+        for (int rd = 0; rd < CT / 4; rd++) {
+          const int r = rd * 4 + grp;
+          const int t = T0 + c * CT + r;
+          if (t >= t0 && t < t1) {
+            float vv[DPL];
+            if constexpr (NP >= 16) {
+#pragma unroll
+              for (int pp = 0; pp < PPL; pp++) {
+                const int piece = e16 + 16 * pp;
+                const h8 hv = __builtin_bit_cast(h8, buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) vv[pp * 8 + e] = (float)hv[e];
+              }
+            } else {
+              const int piece = e16 >> 1;
+              const u32x4 pv = buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))];
+              const u32x2 half = (e16 & 1) ? u32x2{pv[2], pv[3]} : u32x2{pv[0], pv[1]};
+              const h4 hv = __builtin_bit_cast(h4, half);
+#pragma unroll
+              for (int e = 0; e < 4; e++) vv[e] = (float)hv[e];
+            }
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+              const float p = sc[h * split + (t - t0)];
+              l[h] = l[h] + p;
+#pragma unroll
+              for (int d = 0; d < DPL; d++) o[h][d] = __builtin_fmaf(p, vv[d], o[h][d]);
+            }
+          }
         }
       }
     }
@@ -885,8 +1043,15 @@ __global__ __launch_bounds__(64) void k_attn_split(
     if (grp == 0) {
 #pragma unroll
       for (int h = 0; h < G; h++) {
+        if constexpr (NP >= 16) {
 #pragma unroll
-        for (int d = 0; d < DPL; d++) pr[h * (HD + 2) + e16 * DPL + d] = o[h][d];
+          for (int pp = 0; pp < PPL; pp++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) pr[h * (HD + 2) + (e16 + 16 * pp) * 8 + e] = o[h][pp * 8 + e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) pr[h * (HD + 2) + e16 * 4 + e] = o[h][e];
+        }
         if (e16 == 0) {
           pr[h * (HD + 2) + HD] = mx[h];
           pr[h * (HD + 2) + HD + 1] = l[h];
@@ -901,11 +1066,12 @@ template <int HD, int G, int LPT>
 static void launch_split_t(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
                            const uint16_t* vp, const int32_t* pt, const int32_t* len,
                            const int32_t* tab, float* part, int max_items) {
-  int grid = max_items < 8192 ? max_items : 8192;
+  int grid = max_items < 4096 ? max_items : 4096;
   if (grid < 1) grid = 1;
-  size_t lds = sizeof(float) * G * g.split;
+  const int pg_cap = (g.split + g.page_size - 1) / g.page_size + 2;
+  size_t lds = (size_t)4 * 16 * (HD / 8) * 16 + sizeof(float) * G * g.split + sizeof(int32_t) * pg_cap;
   hipLaunchKernelGGL((k_attn_split<HD, G, LPT>), dim3(grid), dim3(64), lds, st, g.batch, g.n_kv,
-                     g.page_size, g.pps, g.split, g.scale, q, kp, vp, pt, len, tab, part);
+                     g.page_size, g.pps, g.split, g.scale, q, kp, vp, pt, len, tab, part, pg_cap);
 }
 
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,

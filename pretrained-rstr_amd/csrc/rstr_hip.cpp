@@ -505,7 +505,7 @@ extern "C" int rstr_model_export_linear(rstr_model* m, int32_t layer, int32_t ro
           for (int i = 0; i < 32; i++) o[i] = (int8_t)q[i];
         }
       }
-      if (ws) ws[(size_t)r * nb + b] = hs[(((size_t)ct * nb4 + bq) * 16 + nn) * 4 + bb];
+      if (ws) ws[(size_t)r * nb + b] = hs[((((size_t)ct * nb4 + bq) * 4 + (nn >> 2)) * 4 + bb) * 4 + (nn & 3)];
     }
   }
   return RSTR_OK;
@@ -691,10 +691,10 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   d->kvr = md.n_kv * md.head_dim;
   d->nqkv = d->qd + 2 * d->kvr;
   d->kmax = std::max(md.d_model, std::max(d->qd, md.d_ff));
-  d->s_qkv = qgemm_splits(d->nqkv, d->mpad);
-  d->s_o = qgemm_splits(md.d_model, d->mpad);
-  d->s_gu = qgemm_splits(2 * md.d_ff, d->mpad);
-  d->s_down = qgemm_splits(md.d_model, d->mpad);
+  d->s_qkv = qgemm_splits(d->nqkv, d->mpad, md.weight_bits);
+  d->s_o = qgemm_splits(md.d_model, d->mpad, md.weight_bits);
+  d->s_gu = qgemm_splits(2 * md.d_ff, d->mpad, md.weight_bits);
+  d->s_down = qgemm_splits(md.d_model, d->mpad, md.weight_bits);
   const int s_d = std::max(d->s_o, d->s_down);
   int64_t max_pos_tokens = std::min<int64_t>((int64_t)pps * p->page_size, (int64_t)maxpos + 1);
   int64_t splits = (max_pos_tokens + split - 1) / split + 1;
