@@ -91,18 +91,38 @@ __device__ __forceinline__ float synth_normal(uint64_t key, uint64_t index, doub
 }
 
 // ---- wavefront reductions ----------------------------------------------------
+// lane exchange v[lane ^ M]: quad permutes for M < 4 (DPP), the swizzle
+// unit inside 32-lane halves for M < 32, bpermute across halves.
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+  if constexpr (M == 1)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  else if constexpr (M == 2)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  else if constexpr (M < 32)
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (M << 10)));
+  else
+    return __shfl_xor(v, M, 64);
+}
+
 // xor butterfly: level m combines lanes i and i^m.  Because fp add commutes,
 // both lanes hold the same value and the result is the balanced pairwise tree
 // over lane order.
 __device__ __forceinline__ float wave_tree_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = v + __shfl_xor(v, m, 64);
-  return v;
+  v = v + xor_lane<1>(v);
+  v = v + xor_lane<2>(v);
+  v = v + xor_lane<4>(v);
+  v = v + xor_lane<8>(v);
+  v = v + xor_lane<16>(v);
+  return v + xor_lane<32>(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, xor_lane<1>(v));
+  v = fmaxf(v, xor_lane<2>(v));
+  v = fmaxf(v, xor_lane<4>(v));
+  v = fmaxf(v, xor_lane<8>(v));
+  v = fmaxf(v, xor_lane<16>(v));
+  return fmaxf(v, xor_lane<32>(v));
 }
 
 }  // namespace rstr

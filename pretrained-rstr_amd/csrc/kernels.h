@@ -83,7 +83,7 @@ hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const int32_t* page_table, const int32_t* lengths,
                              const int32_t* lane_tab, float* part, int max_items);
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
-                             const int32_t* lane_tab, const float* part, float* out_f32,
+                             int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q);
 
 // tail, priming, pages
@@ -102,7 +102,8 @@ hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
                                  int64_t page_elems, const uint16_t* tmpl, const int32_t* pages,
                                  int npages, uint64_t seed);
 
-// lane table layout (int32): lo[B] k0[B] nsplit[B] base[B+1]
-inline int lane_tab_words(int batch) { return 4 * batch + 1; }
+// lane table layout (int32): lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]; cbase
+// is the prefix of item costs that the split kernel divides between waves.
+inline int lane_tab_words(int batch) { return 5 * batch + 2; }
 
 }  // namespace rstr

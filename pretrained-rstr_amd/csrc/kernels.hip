@@ -528,9 +528,9 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
 __device__ __forceinline__ void quant_store(f4 y, bool valid, int c, int row, int nb, int mpad,
                                             _Float16* __restrict__ Q, float* __restrict__ S) {
   float a = valid ? fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3]))) : 0.0f;
-  a = fmaxf(a, __shfl_xor(a, 1, 64));
-  a = fmaxf(a, __shfl_xor(a, 2, 64));
-  a = fmaxf(a, __shfl_xor(a, 4, 64));
+  a = fmaxf(a, xor_lane<1>(a));
+  a = fmaxf(a, xor_lane<2>(a));
+  a = fmaxf(a, xor_lane<4>(a));
   if (!valid) return;
   float d = a / 127.0f;
   float id = (d != 0.0f) ? 1.0f / d : 0.0f;
@@ -774,15 +774,20 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
 // Work item = (lane, kv head, history split of `split` tokens); items are
 // packed by a device-side lane table so ragged lanes cost only their pages.
 // ===========================================================================
+// Per-lane item table.  Item (lane b, kv head h, split k) has cost
+// (visible tokens of the split) + RSTR_ITEM_OVH; cbase is the cost prefix the
+// split kernel partitions into equal shares, one per resident wave.
+#define RSTR_ITEM_OVH 16
 __global__ void k_attn_prep(int batch, int split, int window, int n_kv,
                             const int32_t* __restrict__ lengths, int32_t* __restrict__ tab) {
-  // tab: lo[B] k0[B] nsplit[B] base[B+1]
+  // tab: lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]
   if (threadIdx.x != 0) return;
   int32_t* lo = tab;
   int32_t* k0 = tab + batch;
   int32_t* ns = tab + 2 * batch;
   int32_t* base = tab + 3 * batch;
-  int32_t acc = 0;
+  int32_t* cbase = tab + 4 * batch + 1;
+  int32_t acc = 0, cacc = 0;
   for (int b = 0; b < batch; b++) {
     int len = lengths[b];
     int l0 = 0, kk0 = 0, n = 0;
@@ -795,9 +800,48 @@ __global__ void k_attn_prep(int batch, int split, int window, int n_kv,
     k0[b] = kk0;
     ns[b] = n;
     base[b] = acc;
+    cbase[b] = cacc;
     acc += n * n_kv;
+    cacc += n_kv * ((len - l0) + n * RSTR_ITEM_OVH);
   }
   base[batch] = acc;
+  cbase[batch] = cacc;
+}
+
+// First item whose starting cost is >= x (items in (lane, kv head, split)
+// order; within one kv head of lane b the splits cost tok0+OVH, then
+// split+OVH each, the last one possibly less).
+__device__ __forceinline__ int attn_first_item(int x, int batch, int n_kv, int split,
+                                               const int32_t* __restrict__ lo_t,
+                                               const int32_t* __restrict__ k0_t,
+                                               const int32_t* __restrict__ ns_t,
+                                               const int32_t* __restrict__ base,
+                                               const int32_t* __restrict__ cbase,
+                                               const int32_t* __restrict__ lengths) {
+  if (x >= cbase[batch]) return base[batch];
+  int lo = 0, hi = batch;  // last lane with cbase <= x
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cbase[mid] <= x) lo = mid; else hi = mid;
+  }
+  int b = lo;
+  while (b < batch && ns_t[b] == 0) b++;  // empty lanes own no cost
+  if (b >= batch) return base[batch];
+  const int ns = ns_t[b];
+  const int len = lengths[b];
+  const int l0 = lo_t[b];
+  const int kc = (len - l0) + ns * RSTR_ITEM_OVH;  // cost of one kv head's splits
+  const int rel = max(0, x - cbase[b]);
+  int h = rel / kc;
+  const int r2 = rel - h * kc;
+  const int c0 = min(len, (k0_t[b] + 1) * split) - l0 + RSTR_ITEM_OVH;  // first split
+  int idx;
+  if (r2 <= 0) idx = 0;
+  else if (r2 <= c0) idx = 1;
+  else idx = 1 + (r2 - c0 + split + RSTR_ITEM_OVH - 1) / (split + RSTR_ITEM_OVH);
+  if (idx >= ns) { idx = 0; h++; }
+  if (h >= n_kv) return base[b + 1];
+  return base[b] + h * ns + idx;
 }
 
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
@@ -830,216 +874,356 @@ __device__ __forceinline__ int attn_swz(int r) {
 
 #define RSTR_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <int HD, int G, int LPT>
+// Geometry of one work item (all values wave-uniform).
+struct AttnItem {
+  int b, kvh, idx, t0, t1, T0, nch;
+};
+
+// Item fields are wave-uniform; readfirstlane keeps them in scalar registers
+// so the table lookups stay scalar loads (a vector load here would make the
+// compiler wait for every outstanding DMA).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ void attn_item_fill(AttnItem& it, int split,
+                                               const int32_t* __restrict__ lo_t,
+                                               const int32_t* __restrict__ k0_t,
+                                               const int32_t* __restrict__ lengths) {
+  it.b = uni(it.b);
+  it.kvh = uni(it.kvh);
+  it.idx = uni(it.idx);
+  const int k = uni(k0_t[it.b]) + it.idx;
+  it.t0 = uni(max(lo_t[it.b], k * split));
+  it.t1 = uni(min(lengths[it.b], (k + 1) * split));
+  it.T0 = it.t0 & ~15;
+  it.nch = (it.t1 - it.T0 + 15) / 16;
+}
+
+// The item after `it` in (lane, kv head, split) order (lanes without
+// visible tokens hold no items).  Callers stop at their range end, so the
+// lane index never runs past the last lane that holds items.
+__device__ __forceinline__ void attn_item_next(AttnItem& it, int batch, int n_kv, int split,
+                                               const int32_t* __restrict__ lo_t,
+                                               const int32_t* __restrict__ k0_t,
+                                               const int32_t* __restrict__ ns_t,
+                                               const int32_t* __restrict__ lengths) {
+  int b = uni(it.b);
+  if (++it.idx >= uni(ns_t[b])) {
+    it.idx = 0;
+    if (++it.kvh >= n_kv) {
+      it.kvh = 0;
+      do { b = uni(b + 1); } while (b < batch - 1 && uni(ns_t[b]) == 0);
+    }
+  }
+  it.b = b;
+  attn_item_fill(it, split, lo_t, k0_t, lengths);
+}
+
+__device__ __forceinline__ AttnItem attn_item(int item, int batch, int split,
+                                              const int32_t* __restrict__ lo_t,
+                                              const int32_t* __restrict__ k0_t,
+                                              const int32_t* __restrict__ ns_t,
+                                              const int32_t* __restrict__ base,
+                                              const int32_t* __restrict__ lengths) {
+  int lo = 0, hi = batch;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (base[mid] <= item) lo = mid; else hi = mid;
+  }
+  AttnItem it;
+  it.b = lo;
+  const int ns = ns_t[lo];
+  const int rel = item - base[lo];
+  it.kvh = rel / ns;
+  it.idx = rel % ns;
+  attn_item_fill(it, split, lo_t, k0_t, lengths);
+  return it;
+}
+
+template <int HD, int G, int LPT, bool PG16, int RB>
 __global__ __launch_bounds__(64) void k_attn_split(
     int batch, int n_kv, int page_size, int pps, int split, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ lengths,
-    const int32_t* __restrict__ tab, float* __restrict__ part, int pg_cap) {
+    const int32_t* __restrict__ tab, float* __restrict__ part) {
   constexpr int NP = HD / 8;             // 16-byte pieces per row
   constexpr int CT = 16;                 // tokens per chunk
   constexpr int CU16 = CT * NP;          // 16-byte units per chunk
   constexpr int LPC = CU16 / 64;         // DMA instructions per chunk
-  constexpr int RB = 4;                  // ring buffers
   constexpr int NCL = NP / LPT;          // QK pieces per lane
   constexpr int NSL = 16 / LPT;          // slice slots per lane
   constexpr int TPP = 64 / LPT;          // tokens per QK pass
   constexpr int PPL = NP >= 16 ? NP / 16 : 1;   // PV pieces per lane (HD 64: half a piece)
   constexpr int DPL = HD / 16;           // PV dims per lane
+  constexpr int WAIT_STEADY = ((LPC * (RB - 1)) & 0xF) | (((LPC * (RB - 1)) >> 4) << 14) | 0x0F70;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int QB = (G * HD * 4 + 1023) / 1024;  // 1 KB DMA blocks of one kv group's query
   u32x4* ring = reinterpret_cast<u32x4*>(smem);                        // [RB][CU16]
-  float* sc = reinterpret_cast<float*>(smem + RB * CU16 * 16);          // [G][split]
-  int32_t* s_pg = reinterpret_cast<int32_t*>(sc + G * split);          // [pg_cap]
+  u32x4* qlds = ring + RB * CU16;                                       // [QB][64]
+  float* sc = reinterpret_cast<float*>(qlds + QB * 64);                 // [split][G]
   const int lane = threadIdx.x;
   const int32_t* lo_t = tab;
   const int32_t* k0_t = tab + batch;
   const int32_t* ns_t = tab + 2 * batch;
   const int32_t* base = tab + 3 * batch;
-  const int total = base[batch];
+  const int32_t* cbase = tab + 4 * batch + 1;
   const int kvr = n_kv * HD;
   const int ts = lane / LPT, j = lane % LPT;
   const int grp = lane >> 4, e16 = lane & 15;
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    int lo = 0, hi = batch;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (base[mid] <= item) lo = mid; else hi = mid;
-    }
-    const int b = lo;
-    const int ns = ns_t[b];
-    const int rel = item - base[b];
-    const int kvh = rel / ns;
-    const int k = k0_t[b] + rel % ns;
-    const int len = lengths[b];
-    const int t0 = max(lo_t[b], k * split);
-    const int t1 = min(len, (k + 1) * split);
-    const int T0 = t0 & ~(CT - 1);
-    const int nch = (t1 - T0 + CT - 1) / CT;
-    const int pg0 = t0 / page_size;
-    const int npg = (t1 - 1) / page_size - pg0 + 1;
-    const int32_t* pt = page_table + (size_t)b * pps;
-    for (int i = lane; i < npg; i += 64) s_pg[i] = pt[pg0 + i];
-    const uint16_t* kbase = kp + kvh * HD;
-    const uint16_t* vbase = vp + kvh * HD;
-    __builtin_amdgcn_s_waitcnt(0);  // page ids visible before the first DMA address uses them
-    __syncthreads();
+  // per-lane DMA geometry: row within the chunk and element offset of the
+  // lane's 16-byte piece for each of the chunk's LPC load instructions
+  int dma_r[LPC], dma_off[LPC];
+  uint32_t dma_boff[LPC];  // byte offset from the chunk's first row (one page)
+#pragma unroll
+  for (int u = 0; u < LPC; u++) {
+    const int pos = u * 64 + lane;
+    dma_r[u] = pos / NP;
+    dma_off[u] = ((pos % NP) ^ attn_swz<HD, LPT>(dma_r[u])) * 8;
+    dma_boff[u] = (uint32_t)(dma_r[u] * kvr + dma_off[u]) * 2u;
+  }
 
-    // DMA of stream position s (s < nch: K chunk s, else V chunk s - nch)
-    auto issue = [&](int s) {
-      const bool isk = s < nch;
-      const int c = isk ? s : s - nch;
-      const uint16_t* src = isk ? kbase : vbase;
-      u32x4* dst = ring + (s % RB) * CU16;
-#pragma unroll
-      for (int u = 0; u < LPC; u++) {
-        const int pos = u * 64 + lane;
-        const int r = pos / NP;
-        const int piece = (pos % NP) ^ attn_swz<HD, LPT>(r);
-        const int t = min(max(T0 + c * CT + r, t0), t1 - 1);
-        const int page = s_pg[t / page_size - pg0];
-        const uint16_t* g = src + ((size_t)page * page_size + (t % page_size)) * kvr + piece * 8;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g), RSTR_LDS_PTR(dst + u * 64), 16, 0, 0);
-      }
-    };
+  // Static cost-balanced partition: wave w takes the items whose starting
+  // cost lies in [w*C/R, (w+1)*C/R), a contiguous run of items.
+  const int64_t ctot = cbase[batch];
+  const int x0 = (int)(ctot * blockIdx.x / gridDim.x);
+  const int x1 = (int)(ctot * (blockIdx.x + 1) / gridDim.x);
+  const int i_begin = attn_first_item(x0, batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase, lengths);
+  const int i_end = attn_first_item(x1, batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase, lengths);
+  if (i_begin >= i_end) return;
 
-    // query slices for the G heads of this kv group
-    float qv[G][NCL][8];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      const float* qh = q + ((size_t)b * (n_kv * G) + kvh * G + h) * HD;
-#pragma unroll
-      for (int i = 0; i < NCL; i++) {
-        const int cch = j + LPT * i;
-        const f4 a = *reinterpret_cast<const f4*>(qh + 8 * cch);
-        const f4 bq = *reinterpret_cast<const f4*>(qh + 8 * cch + 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = bq[e]; }
-      }
-    }
-    float mx[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) mx[h] = -__builtin_inff();
-    float o[G][DPL], l[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      l[h] = 0.0f;
-#pragma unroll
-      for (int d = 0; d < DPL; d++) o[h][d] = 0.0f;
-    }
+  // One continuous stream per wave: the positions of item i are its K
+  // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
+  // consumer across item boundaries, so the ring never drains between items.
+  int pi = i_begin, ppos = 0;  // producer cursor
+  AttnItem gp = attn_item(pi, batch, split, lo_t, k0_t, ns_t, base, lengths);
+  int issued = 0;
+  // page of the producer's next chunk (one page per chunk when page_size % 16 == 0)
+  int pg_next = 0;
+  if constexpr (PG16) pg_next = page_table[(size_t)gp.b * pps + gp.T0 / page_size];
 
-    const int npos = 2 * nch;
+#define RSTR_ATTN_ISSUE()                                                                         \
+  do {                                                                                            \
+    const bool isk_ = ppos < gp.nch;                                                              \
+    const int c_ = isk_ ? ppos : ppos - gp.nch;                                                   \
+    const uint16_t* src_ = (isk_ ? kp : vp) + gp.kvh * HD;                                        \
+    u32x4* dst_ = ring + (issued % RB) * CU16;                                                    \
+    const int tb_ = gp.T0 + c_ * CT;                                                              \
+    if constexpr (PG16) {                                                                         \
+      const char* cb_ = reinterpret_cast<const char*>(                                            \
+          src_ + ((size_t)pg_next * page_size + (tb_ % page_size)) * kvr);                        \
+      _Pragma("unroll") for (int u = 0; u < LPC; u++)                                             \
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(cb_ + dma_boff[u]),        \
+                                         RSTR_LDS_PTR(dst_ + u * 64), 16, 0, 0);                  \
+    } else {                                                                                      \
+      const int32_t* prow_ = page_table + (size_t)gp.b * pps;                                     \
+      _Pragma("unroll") for (int u = 0; u < LPC; u++) {                                           \
+        const int t_ = min(max(tb_ + dma_r[u], gp.t0), gp.t1 - 1);                                \
+        const int page_ = prow_[t_ / page_size];                                                  \
+        const uint16_t* g_ = src_ + ((size_t)page_ * page_size + (t_ % page_size)) * kvr + dma_off[u]; \
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g_), RSTR_LDS_PTR(dst_ + u * 64), 16, 0, 0); \
+      }                                                                                           \
+    }                                                                                             \
+    issued++;                                                                                     \
+    if (++ppos == 2 * gp.nch) {                                                                   \
+      ppos = 0;                                                                                   \
+      if (++pi < i_end) attn_item_next(gp, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);         \
+    }                                                                                             \
+    if constexpr (PG16) {                                                                         \
+      if (pi < i_end) {                                                                           \
+        const int cn_ = ppos < gp.nch ? ppos : ppos - gp.nch;                                     \
+        pg_next = page_table[(size_t)gp.b * pps + (gp.T0 + cn_ * CT) / page_size];                \
+      }                                                                                           \
+    }                                                                                             \
+  } while (0)
+
+  for (int k = 0; k < RB - 1; k++)
+    if (pi < i_end) RSTR_ATTN_ISSUE();
+
+  // consumer
+  int ci = i_begin, cpos = 0, consumed = 0;
+  AttnItem gc = attn_item(i_begin, batch, split, lo_t, k0_t, ns_t, base, lengths);
+  float qv[G][NCL][8];
+  // A kv group's G query rows are contiguous: they reach LDS by QB DMA
+  // instructions (lanes past the end re-read the last piece).
+#define RSTR_ATTN_DMA_Q(IT)                                                                       \
+  do {                                                                                            \
+    const float* qg_ = q + ((size_t)(IT).b * (n_kv * G) + (IT).kvh * G) * HD;                     \
+    _Pragma("unroll") for (int u = 0; u < QB; u++) {                                              \
+      const int pc_ = min(u * 64 + lane, G * HD / 4 - 1);                                         \
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(qg_ + 4 * pc_),              \
+                                       RSTR_LDS_PTR(qlds + u * 64), 16, 0, 0);                    \
+    }                                                                                             \
+  } while (0)
+#define RSTR_ATTN_READ_Q()                                                                        \
+  do {                                                                                            \
+    const float* qf_ = reinterpret_cast<const float*>(qlds);                                      \
+    _Pragma("unroll") for (int h = 0; h < G; h++)                                                 \
+      _Pragma("unroll") for (int i = 0; i < NCL; i++) {                                           \
+        const int cch = j + LPT * i;                                                              \
+        const f4 a = *reinterpret_cast<const f4*>(qf_ + h * HD + 8 * cch);                        \
+        const f4 bq = *reinterpret_cast<const f4*>(qf_ + h * HD + 8 * cch + 4);                   \
+        _Pragma("unroll") for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = bq[e]; } \
+      }                                                                                           \
+  } while (0)
+  RSTR_ATTN_DMA_Q(gc);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): first query and first chunks
+  __asm__ __volatile__("" ::: "memory");
+  RSTR_ATTN_READ_Q();
+  int q_dma_step = -RB;  // consumer step at which the next query DMA was issued
+  float mx[G], o[G][DPL], l[G];
 #pragma unroll
-    for (int s = 0; s < RB - 1; s++)
-      if (s < npos) issue(s);
-    for (int s = 0; s < npos; s++) {
-      if (s + RB - 1 < npos) {
-        // the ring slot being refilled was last read at step s-1, whose LDS
-        // reads have all returned
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        issue(s + RB - 1);
-        // wait until the DMA of position s has landed: RB-1 chunks may remain
-        __builtin_amdgcn_s_waitcnt(((LPC * (RB - 1)) & 0xF) | (((LPC * (RB - 1)) >> 4) << 14) | 0x0F70);
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      }
-      __asm__ __volatile__("" ::: "memory");
-      const u32x4* buf = ring + (s % RB) * CU16;
-      if (s < nch) {
-        // ---- QK over the 16 rows of this chunk --------------------------------
+  for (int h = 0; h < G; h++) {
+    mx[h] = -__builtin_inff();
+    l[h] = 0.0f;
 #pragma unroll
-        for (int pass = 0; pass < CT / TPP + (CT % TPP ? 1 : 0); pass++) {
-          const int r = pass * TPP + ts;
-          const int t = T0 + s * CT + r;
-          const bool valid = r < CT && t >= t0 && t < t1;
-          const int rr = r < CT ? r : CT - 1;
-          float sv[G][NSL];
+    for (int d = 0; d < DPL; d++) o[h][d] = 0.0f;
+  }
+
+  while (true) {
+    if (pi < i_end) {
+      // the ring slot being refilled was last read one step ago; its LDS
+      // reads (and the prefetched page id) have all returned
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      RSTR_ATTN_ISSUE();
+      __builtin_amdgcn_s_waitcnt(WAIT_STEADY);  // position `consumed` has landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stream is draining
+    }
+    __asm__ __volatile__("" ::: "memory");
+    const u32x4* buf = ring + (consumed % RB) * CU16;
+    const int t0 = gc.t0, t1 = gc.t1;
+    if (cpos < gc.nch) {
+      // ---- QK over the 16 rows of this chunk --------------------------------
+#pragma unroll
+      for (int pass = 0; pass < CT / TPP + (CT % TPP ? 1 : 0); pass++) {
+        const int r = pass * TPP + ts;
+        const int t = gc.T0 + cpos * CT + r;
+        const bool valid = r < CT && t >= t0 && t < t1;
+        const int rr = r < CT ? r : CT - 1;
+        float sv[G][NSL];
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+          for (int u = 0; u < NSL; u++) sv[h][u] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCL; i++) {
+          const int piece = j + LPT * i;
+          const h8 kv = __builtin_bit_cast(h8, buf[rr * NP + (piece ^ attn_swz<HD, LPT>(rr))]);
 #pragma unroll
           for (int h = 0; h < G; h++)
 #pragma unroll
-            for (int u = 0; u < NSL; u++) sv[h][u] = 0.0f;
-#pragma unroll
-          for (int i = 0; i < NCL; i++) {
-            const int piece = j + LPT * i;
-            const h8 kv = __builtin_bit_cast(h8, buf[rr * NP + (piece ^ attn_swz<HD, LPT>(rr))]);
-#pragma unroll
-            for (int h = 0; h < G; h++)
-#pragma unroll
-              for (int e = 0; e < 8; e++)
-                sv[h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[e], sv[h][i % NSL]);
-          }
-#pragma unroll
-          for (int h = 0; h < G; h++) {
-            float v;
-            if constexpr (LPT == 4) v = (sv[h][0] + sv[h][2]) + (sv[h][1] + sv[h][3]);
-            else if constexpr (LPT == 8) v = sv[h][0] + sv[h][1];
-            else v = sv[h][0];
-#pragma unroll
-            for (int m = LPT / 2; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            const float score = v * scale;
-            if (valid) {
-              if (j == 0) sc[h * split + (t - t0)] = score;
-              mx[h] = fmaxf(mx[h], score);
-            }
-          }
+            for (int e = 0; e < 8; e++)
+              sv[h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[e], sv[h][i % NSL]);
         }
-        if (s == nch - 1) {
-          // ---- softmax numerators over the whole split ----------------------------
+        float scv[G];
 #pragma unroll
-          for (int h = 0; h < G; h++) mx[h] = wave_max(mx[h]);
-          __syncthreads();
-          const int nt = t1 - t0;
-          for (int i = lane; i < nt; i += 64)
-#pragma unroll
-            for (int h = 0; h < G; h++) sc[h * split + i] = dexp(sc[h * split + i] - mx[h]);
-          __syncthreads();
+        for (int h = 0; h < G; h++) {
+          float v;
+          if constexpr (LPT == 4) v = (sv[h][0] + sv[h][2]) + (sv[h][1] + sv[h][3]);
+          else if constexpr (LPT == 8) v = sv[h][0] + sv[h][1];
+          else v = sv[h][0];
+          if constexpr (LPT >= 16) v = v + xor_lane<8>(v);
+          if constexpr (LPT >= 8) v = v + xor_lane<4>(v);
+          v = v + xor_lane<2>(v);
+          v = v + xor_lane<1>(v);
+          scv[h] = v * scale;
+          if (valid) mx[h] = fmaxf(mx[h], scv[h]);
         }
-      } else {
-        // ---- PV over the 16 rows of this chunk: 4 rounds of one row per group ----
-        const int c = s - nch;
+        if (valid && j == 0) {
+          float* dst = sc + (size_t)(t - t0) * G;
+          if constexpr (G % 4 == 0) {
 #pragma unroll
-        for (int rd = 0; rd < CT / 4; rd++) {
-          const int r = rd * 4 + grp;
-          const int t = T0 + c * CT + r;
-          if (t >= t0 && t < t1) {
-            float vv[DPL];
-            if constexpr (NP >= 16) {
+            for (int h4 = 0; h4 < G; h4 += 4)
+              *reinterpret_cast<f4*>(dst + h4) = f4{scv[h4], scv[h4 + 1], scv[h4 + 2], scv[h4 + 3]};
+          } else {
 #pragma unroll
-              for (int pp = 0; pp < PPL; pp++) {
-                const int piece = e16 + 16 * pp;
-                const h8 hv = __builtin_bit_cast(h8, buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))]);
-#pragma unroll
-                for (int e = 0; e < 8; e++) vv[pp * 8 + e] = (float)hv[e];
-              }
-            } else {
-              const int piece = e16 >> 1;
-              const u32x4 pv = buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))];
-              const u32x2 half = (e16 & 1) ? u32x2{pv[2], pv[3]} : u32x2{pv[0], pv[1]};
-              const h4 hv = __builtin_bit_cast(h4, half);
-#pragma unroll
-              for (int e = 0; e < 4; e++) vv[e] = (float)hv[e];
-            }
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-              const float p = sc[h * split + (t - t0)];
-              l[h] = l[h] + p;
-#pragma unroll
-              for (int d = 0; d < DPL; d++) o[h][d] = __builtin_fmaf(p, vv[d], o[h][d]);
-            }
+            for (int h = 0; h < G; h++) dst[h] = scv[h];
           }
         }
       }
+      if (cpos == gc.nch - 1) {
+        // ---- softmax numerators over the whole split ----------------------------
+#pragma unroll
+        for (int h = 0; h < G; h++) mx[h] = wave_max(mx[h]);
+        // The workgroup is this one wave, whose LDS accesses execute in
+        // program order: a compiler barrier orders the score writes and reads
+        // (a workgroup barrier would also wait for every DMA in flight).
+        __asm__ __volatile__("" ::: "memory");
+        const int nt = t1 - t0;
+        for (int i = lane; i < nt; i += 64)
+#pragma unroll
+          for (int h = 0; h < G; h++) sc[i * G + h] = dexp(sc[i * G + h] - mx[h]);
+        __asm__ __volatile__("" ::: "memory");
+        // the next item's query: its DMA lands while this item's V chunks run
+        // (qv itself is reloaded from LDS when the next item starts)
+        if (ci + 1 < i_end) {
+          AttnItem gn = gc;
+          attn_item_next(gn, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);
+          RSTR_ATTN_DMA_Q(gn);
+          q_dma_step = consumed;
+        }
+      }
+    } else {
+      // ---- PV over the 16 rows of this chunk: 4 rounds of one row per group ----
+      // Interior chunks hold only visible rows.  In the first and last chunk
+      // a row outside [t0, t1) contributes p = 0 times v = 0, which leaves
+      // o and l unchanged (they are never -0), without branching per lane.
+      const int c = cpos - gc.nch;
+      const bool edge = (c == 0) || (c == gc.nch - 1);
+#define RSTR_PV_ROUNDS(MASK)                                                                      \
+      _Pragma("unroll") for (int rd = 0; rd < CT / 4; rd++) {                                     \
+        const int r = rd * 4 + grp;                                                               \
+        const int t = gc.T0 + c * CT + r;                                                         \
+        const bool ok = !(MASK) || (t >= t0 && t < t1);                                           \
+        float vv[DPL];                                                                            \
+        if constexpr (NP >= 16) {                                                                 \
+          _Pragma("unroll") for (int pp = 0; pp < PPL; pp++) {                                    \
+            const int piece = e16 + 16 * pp;                                                      \
+            const h8 hv = __builtin_bit_cast(h8, buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))]);   \
+            _Pragma("unroll") for (int e = 0; e < 8; e++) vv[pp * 8 + e] = ok ? (float)hv[e] : 0.0f; \
+          }                                                                                       \
+        } else {                                                                                  \
+          const int piece = e16 >> 1;                                                             \
+          const u32x4 pv = buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))];                          \
+          const u32x2 half = (e16 & 1) ? u32x2{pv[2], pv[3]} : u32x2{pv[0], pv[1]};               \
+          const h4 hv = __builtin_bit_cast(h4, half);                                             \
+          _Pragma("unroll") for (int e = 0; e < 4; e++) vv[e] = ok ? (float)hv[e] : 0.0f;         \
+        }                                                                                         \
+        float pr[G];                                                                              \
+        const float* ps_ = sc + (size_t)(ok ? t - t0 : 0) * G;                                    \
+        if constexpr (G % 4 == 0) {                                                               \
+          _Pragma("unroll") for (int h4 = 0; h4 < G; h4 += 4) {                                   \
+            const f4 p4 = *reinterpret_cast<const f4*>(ps_ + h4);                                 \
+            _Pragma("unroll") for (int e = 0; e < 4; e++) pr[h4 + e] = ok ? p4[e] : 0.0f;         \
+          }                                                                                       \
+        } else {                                                                                  \
+          _Pragma("unroll") for (int h = 0; h < G; h++) pr[h] = ok ? ps_[h] : 0.0f;               \
+        }                                                                                         \
+        _Pragma("unroll") for (int h = 0; h < G; h++) {                                           \
+          l[h] = l[h] + pr[h];                                                                    \
+          _Pragma("unroll") for (int d = 0; d < DPL; d++) o[h][d] = __builtin_fmaf(pr[h], vv[d], o[h][d]); \
+        }                                                                                         \
+      }
+      if (edge) {
+        RSTR_PV_ROUNDS(true)
+      } else {
+        RSTR_PV_ROUNDS(false)
+      }
+#undef RSTR_PV_ROUNDS
     }
+    consumed++;
+    if (++cpos < 2 * gc.nch) continue;
+    // ---- item complete: combine lane groups, write the partial ---------------
 #pragma unroll
     for (int h = 0; h < G; h++) {
-      l[h] = l[h] + __shfl_xor(l[h], 16, 64);
-      l[h] = l[h] + __shfl_xor(l[h], 32, 64);
+      l[h] = l[h] + xor_lane<16>(l[h]);
+      l[h] = l[h] + xor_lane<32>(l[h]);
 #pragma unroll
       for (int d = 0; d < DPL; d++) {
-        o[h][d] = o[h][d] + __shfl_xor(o[h][d], 16, 64);
-        o[h][d] = o[h][d] + __shfl_xor(o[h][d], 32, 64);
+        o[h][d] = o[h][d] + xor_lane<16>(o[h][d]);
+        o[h][d] = o[h][d] + xor_lane<32>(o[h][d]);
       }
     }
-    float* pr = part + (size_t)item * G * (HD + 2);
+    float* prt = part + (size_t)ci * G * (HD + 2);
     if (grp == 0) {
 #pragma unroll
       for (int h = 0; h < G; h++) {
@@ -1047,31 +1231,75 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #pragma unroll
           for (int pp = 0; pp < PPL; pp++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) pr[h * (HD + 2) + (e16 + 16 * pp) * 8 + e] = o[h][pp * 8 + e];
+            for (int e = 0; e < 8; e++) prt[h * (HD + 2) + (e16 + 16 * pp) * 8 + e] = o[h][pp * 8 + e];
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; e++) pr[h * (HD + 2) + e16 * 4 + e] = o[h][e];
+          for (int e = 0; e < 4; e++) prt[h * (HD + 2) + e16 * 4 + e] = o[h][e];
         }
         if (e16 == 0) {
-          pr[h * (HD + 2) + HD] = mx[h];
-          pr[h * (HD + 2) + HD + 1] = l[h];
+          prt[h * (HD + 2) + HD] = mx[h];
+          prt[h * (HD + 2) + HD + 1] = l[h];
         }
       }
     }
-    __syncthreads();
+    if (++ci >= i_end) break;
+    cpos = 0;
+    attn_item_next(gc, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);
+    // the query DMA is complete once a position issued after it has been
+    // waited for; position p is issued at consumer step p - (RB - 1)
+    if (consumed - 1 < q_dma_step + RB) __builtin_amdgcn_s_waitcnt(0x0F70);
+    __asm__ __volatile__("" ::: "memory");
+    RSTR_ATTN_READ_Q();
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      mx[h] = -__builtin_inff();
+      l[h] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DPL; d++) o[h][d] = 0.0f;
+    }
   }
+#undef RSTR_ATTN_ISSUE
+#undef RSTR_ATTN_DMA_Q
+#undef RSTR_ATTN_READ_Q
 }
+
+// Resident workgroups per CU of one split-kernel instantiation (cached).
+template <typename K>
+static int attn_resident_grid(K kernel, size_t lds) {
+  static int cus = 0;
+  static size_t cached_lds = 0;
+  static int per_cu = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cus <= 0) cus = 256;
+  }
+  if (cached_lds != lds || per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64, lds) != hipSuccess || n <= 0) n = 2;
+    per_cu = n;
+    cached_lds = lds;
+  }
+  return cus * per_cu;
+}
+
+// Ring depth: deeper rings keep more rows in flight per wave (fewer waves fit).
+#define RSTR_ATTN_RING 4
 
 template <int HD, int G, int LPT>
 static void launch_split_t(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
                            const uint16_t* vp, const int32_t* pt, const int32_t* len,
                            const int32_t* tab, float* part, int max_items) {
-  int grid = max_items < 4096 ? max_items : 4096;
+  constexpr int RB = RSTR_ATTN_RING;
+  size_t lds = (size_t)RB * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
+               sizeof(float) * G * g.split;
+  auto kern = (g.page_size % 16 == 0) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
+  int grid = attn_resident_grid(kern, lds);
+  if (grid > max_items) grid = max_items;
   if (grid < 1) grid = 1;
-  const int pg_cap = (g.split + g.page_size - 1) / g.page_size + 2;
-  size_t lds = (size_t)4 * 16 * (HD / 8) * 16 + sizeof(float) * G * g.split + sizeof(int32_t) * pg_cap;
-  hipLaunchKernelGGL((k_attn_split<HD, G, LPT>), dim3(grid), dim3(64), lds, st, g.batch, g.n_kv,
-                     g.page_size, g.pps, g.split, g.scale, q, kp, vp, pt, len, tab, part, pg_cap);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64), lds, st, g.batch, g.n_kv, g.page_size, g.pps, g.split,
+                     g.scale, q, kp, vp, pt, len, tab, part);
 }
 
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
@@ -1098,7 +1326,7 @@ hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
 template <int HD>
 __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
                                                    const int32_t* __restrict__ lengths,
-                                                   const int32_t* __restrict__ tab,
+                                                   int32_t* __restrict__ tab,
                                                    const float* __restrict__ part,
                                                    float* __restrict__ out_f32,
                                                    _Float16* __restrict__ Q, float* __restrict__ S,
@@ -1158,7 +1386,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
 }
 
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
-                             const int32_t* lane_tab, const float* part, float* out_f32,
+                             int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q) {
   dim3 grid(g.batch * g.n_q);
   _Float16* Q = out_q ? out_q->q : nullptr;
