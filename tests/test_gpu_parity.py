@@ -411,3 +411,39 @@ def test_copy_page_copies_every_layer_and_slab(sess):
     finally:
         p.close()
         m.close()
+
+
+@pytest.mark.parametrize("case", ["tiny_gemma_q4", "tiny_qwen_q8", "tiny_llama_q4"])
+def test_decode_matches_golden_fixture(sess, case):
+    """The HIP decoder reproduces the committed oracle digests without running
+    the oracle (tests/golden/decode_*.json)."""
+    import hashlib
+    import json
+    import os
+    from golden.make_golden import GEOM, schedule_descriptors
+    print(f"case golden {case}", flush=True)
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"decode_{case}.json")) as f:
+        want = json.load(f)["oracle"]
+    cfg, B, fills, steps = schedule_descriptors(case)
+    g = GEOM
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    m = hip.Model(sess, cfg, seed=g["seed"])
+    p = hip.Pool(m, g["ps"], g["pages"])
+    d = hip.Decoder(m, p, B, g["pps"], g["maxpos"], g["split"])
+    try:
+        if fills:
+            p.fill_synthetic(fills, g["kv_seed"])
+        d.prime_lanes(np.arange(B), (np.arange(B) * 37 + 5) % cfg["vocab"])
+        for (active, desc), ws in zip(steps, want["steps"]):
+            t = d.step_lanes(**desc)
+            act = np.array(active)
+            assert [int(x) for x in t[act]] == ws["tokens"]
+            assert sha(d.logits()[act]) == ws["logits_sha256"]
+        assert sha(d.rows()) == want["rows_sha256"]
+        for layer in range(cfg["n_layers"]):
+            for slab in (0, 1):
+                assert sha(p.pages(slab, layer).view(np.uint16)) == want["pages_sha256"][layer][slab]
+    finally:
+        d.close()
+        p.close()
+        m.close()
