@@ -88,7 +88,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (the decode step "
-                                   "shards as independent replicas, see DESIGN.md)"}))
+                                   "shards as independent per-GPU replicas with their own lanes and "
+                                   "page pools, so one GPU's throughput is the per-replica figure)"}))
         sys.exit(2)
 
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
@@ -141,6 +142,9 @@ def main():
     prof = dec.profile_steps(first, args.profile_steps)
     prof_plan = plan[first:first + args.profile_steps]
     attn_bytes = np.mean([np.mean(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in prof_plan])
+    all_bytes = np.mean([np.mean(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in plan])
+    log(f"attention algorithmic bytes per launch: {all_bytes:.0f} (all {len(plan)} steps), "
+        f"{attn_bytes:.0f} (profiled steps)")
     attn_ms, attn_n = prof["attn_split"]
     attn_avg_ms = attn_ms / max(attn_n, 1)
     attn_gbs = attn_bytes / (attn_avg_ms * 1e-3) / 1e9

@@ -12,7 +12,7 @@
  * is complete before that step's append (paged_attention.clj:351-353).
  *
  * Each entry cites the reference interface it replaces (file:line into the
- * reference repository).  INTEGRATION.md shows the JDK 21 FFM binding.
+ * reference repository).
  */
 #ifndef RSTR_HIP_H
 #define RSTR_HIP_H

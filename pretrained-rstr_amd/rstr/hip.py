@@ -1,7 +1,7 @@
 """ctypes binding of ``librstr_hip.so`` (declared in ``include/rstr_hip.h``).
 
-This is the Python twin of the FFM binding a Clojure caller would use
-(INTEGRATION.md): thin handles, plain int32/f32 arrays, negative status codes
+This is the Python twin of the JDK 21 FFM binding a Clojure caller would use:
+thin handles, plain int32/f32 arrays, negative status codes
 turned into :class:`RstrError` carrying the library's message, the way the
 reference raises ``ex-info``.  No computation happens here; every call goes to
 the HIP library, and loading fails loudly if the library is missing.
