@@ -147,243 +147,281 @@ hipError_t launch_prescale(hipStream_t st, float* out, const float* in, int64_t 
 // of one row (m = lane%16): it needs one activation scale per block and row
 // tile, and the 4 weight scales of its columns per block and column tile.
 
-__device__ __forceinline__ h8 unpack_q4(uint32_t x) {
-  const uint32_t M = 0x000F000Fu, E = 0x64006400u;
-  h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  h2 a = __builtin_bit_cast(h2, (x & M) | E) + off;
-  h2 b = __builtin_bit_cast(h2, ((x >> 4) & M) | E) + off;
-  h2 c = __builtin_bit_cast(h2, ((x >> 8) & M) | E) + off;
-  h2 d = __builtin_bit_cast(h2, ((x >> 12) & M) | E) + off;
+#define RSTR_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// A VGPR holding a constant the compiler cannot fold, so or(and(x, M), E)
+// selects one v_and_or_b32 (M in an SGPR, E in this VGPR).
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+  return r;
+}
+
+// Q4 dword (nibble i at bits 4i carries k_local {0,2,4,6,1,3,5,7}[i]) -> the
+// 8 fp16 integers q - 8 in k order.  Even nibbles: (x & 0x000F000F) | 0x6400
+// is the fp16 value 1024 + n; odd nibbles stay in bits 4..7, giving 1024 + 16n,
+// which one exact packed fma maps to n - 8.  E = 0x64006400.
+__device__ __forceinline__ h8 unpack_q4(uint32_t x, uint32_t E) {
+  const uint32_t x8 = x >> 8;
+  h2 a = __builtin_bit_cast(h2, (x & 0x000F000Fu) | E);
+  h2 b = __builtin_bit_cast(h2, (x & 0x00F000F0u) | E);
+  h2 c = __builtin_bit_cast(h2, (x8 & 0x000F000Fu) | E);
+  h2 d = __builtin_bit_cast(h2, (x8 & 0x00F000F0u) | E);
+  const h2 o1 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 o2 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  a = a + o1;
+  b = __builtin_elementwise_fma(b, s16, o2);
+  c = c + o1;
+  d = __builtin_elementwise_fma(d, s16, o2);
   h8 r = {a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
   return r;
 }
 
-__device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1) {
-  const uint32_t M = 0x00FF00FFu, E = 0x64006400u;
-  h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  uint32_t y0 = x0 ^ 0x80808080u, y1 = x1 ^ 0x80808080u;
-  h2 a = __builtin_bit_cast(h2, (y0 & M) | E) + off;
-  h2 b = __builtin_bit_cast(h2, ((y0 >> 8) & M) | E) + off;
-  h2 c = __builtin_bit_cast(h2, (y1 & M) | E) + off;
-  h2 d = __builtin_bit_cast(h2, ((y1 >> 8) & M) | E) + off;
+// Q8 dword pair (byte i carries k_local {0,2,1,3,4,6,5,7}[i]) -> 8 fp16 q.
+__device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1, uint32_t E) {
+  const uint32_t y0 = x0 ^ 0x80808080u, y1 = x1 ^ 0x80808080u;
+  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  h2 a = __builtin_bit_cast(h2, (y0 & 0x00FF00FFu) | E) + off;
+  h2 b = __builtin_bit_cast(h2, ((y0 >> 8) & 0x00FF00FFu) | E) + off;
+  h2 c = __builtin_bit_cast(h2, (y1 & 0x00FF00FFu) | E) + off;
+  h2 d = __builtin_bit_cast(h2, ((y1 >> 8) & 0x00FF00FFu) | E) + off;
   h8 r = {a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
   return r;
 }
 
-// Workgroup: 4 waves = RH row groups x CG = 4/RH column groups.  A wave owns
-// RT row tiles x CT column tiles over the workgroup's K range, which is NQ
-// whole quarters (split s of 4/NQ); quarters are summed in order with at most
-// two saved tiles.  Activations (fp16 integer fragments and block scales) are
-// staged per chunk of KC blocks (KC = 4, or 1 when a quarter is not a whole
-// number of 4-block groups) through a double-buffered LDS ring shared by the
-// 4 waves; weights and weight scales stream straight into registers one
-// chunk ahead.  With NQ < 4 the workgroups of one column block write 4/NQ
-// output slices that the consumer combines as (s0+s1) or ((s0+s1)+(s2+s3)).
-constexpr int QG_WRT = 8;  // most row tiles per workgroup (128 rows)
-
-template <int RT, int RH, int CT, int BITS, int NQ, int KC>
+// Workgroup: 4 waves over the same RT row tiles (RT*16 rows) and K range, wave
+// w owning column tiles (4*blockIdx.x + w)*CT ..+CT-1.  The K range is NQ whole
+// quarters (split s of 4/NQ); with NQ < 4 the workgroups of one column block
+// write 4/NQ output slices that the consumer combines as (s0+s1) or
+// ((s0+s1)+(s2+s3)).  A chunk is KC blocks (KC = 4, or 1 when a quarter is not
+// a whole number of 4-block groups).  Activation fragments (RT*KC KB) and
+// their scales reach a double-buffered LDS ring by direct-to-LDS DMA, shared
+// by the 4 waves; weights and weight scales stream into registers one chunk
+// ahead.  Row tiles past the batch compute on clamped rows and are never
+// stored, which keeps the hot loop free of branches.
+template <int RT, int CT, int BITS, int NQ, int KC>
 __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W,
-                                                  const uint16_t* __restrict__ Ws,
-                                                  const _Float16* __restrict__ X,
-                                                  const float* __restrict__ Xs, int nb, int nct,
-                                                  int mpad, float* __restrict__ Y, int ldy,
-                                                  int m_rows, size_t slice_stride) {
-  constexpr int CG = 4 / RH;
-  constexpr int WRT = RH * RT;
+                                                const uint16_t* __restrict__ Ws,
+                                                const _Float16* __restrict__ X,
+                                                const float* __restrict__ Xs, int nb, int nct,
+                                                int mpad, float* __restrict__ Y, int ldy,
+                                                int m_rows, size_t slice_stride) {
   constexpr int DW = BITS == 4 ? 1 : 2;
-  constexpr int APT = (WRT * KC * 64 + 255) / 256;  // 16-byte act pieces per thread per chunk
-  constexpr int XPT = (WRT * KC * 16 + 255) / 256;  // activation scales per thread per chunk
-  __shared__ u32x4 s_act[2][WRT * KC * 64];         // [buf][rt][kc][64 lanes x 16 B]
-  __shared__ float s_xs[2][KC][WRT * 16];
+  constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
+  constexpr int XS_N = RT * 16 * KC;               // activation scales per chunk
+  constexpr int XS_I = (XS_N + 63) / 64;           // dword DMA instructions for them
+  constexpr int BUF_U4 = ACT_KB * 64 + XS_I * 16;  // u32x4 units per ring buffer
+  constexpr int AI = (ACT_KB + 3) / 4;             // activation DMAs per wave
+  __shared__ u32x4 ring[2 * BUF_U4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nn = lane & 15, g = lane >> 4;
-  const int cg = wave % CG, rh = wave / CG;
-  const int ct0 = (blockIdx.x * CG + cg) * CT;
+  const int ct0 = (blockIdx.x * 4 + wave) * CT;
   const int split = blockIdx.y;
   const int rg = blockIdx.z;
-  const int mt = min(WRT, (mpad >> 4) - rg * WRT);  // row tiles in this group
+  const int row0 = rg * RT * 16;
+  const int mt = min(RT, (mpad >> 4) - rg * RT);
   const int nb4 = nb >> 2, qs = nb >> 2;
-  const int b_begin = split * NQ * qs;
-  const int cpq = qs / KC;                          // chunks per quarter
+  const int cpq = qs / KC;
   const int nchunk = NQ * cpq;
-  const int row0 = rg * WRT * 16;
-  const u32x4* Xg = reinterpret_cast<const u32x4*>(X) + (size_t)rg * WRT * nb * 64;
-  int ctl[CT];
+  const int b_begin = split * NQ * qs;
+  const uint32_t E = opaque_vgpr(0x64006400u);
+
+  // per-lane DMA sources and weight offsets (chunk-invariant parts)
+  int xs_off[XS_I];
 #pragma unroll
-  for (int c = 0; c < CT; c++) ctl[c] = min(ct0 + c, nct - 1);  // clamped for loads
+  for (int u = 0; u < XS_I; u++) {
+    const int e = (u * 64 + lane) % XS_N;
+    const int kc = e / (16 * RT), n2 = (e / RT) % 16, rt = min(e % RT, mt - 1);
+    xs_off[u] = kc * mpad + row0 + rt * 16 + n2;
+  }
+  const _Float16* xsrc[AI];  // wave-uniform bases; each lane adds lane*16 bytes
+#pragma unroll
+  for (int i = 0; i < AI; i++) {
+    const int a = min(wave + 4 * i, ACT_KB - 1);
+    const int rt = min(a / KC, mt - 1), kc = a % KC;
+    xsrc[i] = X + ((size_t)(rg * RT + rt) * nb + b_begin + kc) * 512;
+  }
+  const uint32_t* wsrc[CT];  // wave-uniform
+  const uint32_t* ssrc[CT];
+#pragma unroll
+  for (int c = 0; c < CT; c++) {
+    const int ctl = min(ct0 + c, nct - 1);
+    const int bq0 = b_begin >> 2;
+    wsrc[c] = W + ((size_t)ctl * nb4 + bq0) * 256 * DW;
+    ssrc[c] = reinterpret_cast<const uint32_t*>(Ws + ((size_t)ctl * nb4 + bq0) * 64);
+  }
+  const int wlane = (g * 16 + nn) * 4 * DW;  // dwords
+  const int slane = g * 8;                   // dwords
+
+  auto issue_dma = [&](int ch, int buf) {
+    u32x4* base = ring + buf * BUF_U4;
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+      const int a = wave + 4 * i;
+      if (ACT_KB % 4 == 0 || a < ACT_KB)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xsrc[i] + (size_t)ch * KC * 512 + lane * 8),
+                                         RSTR_LDS_PTR(base + a * 64), 16, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < XS_I; u++) {
+      if ((u & 3) == wave)
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const void*>(Xs + (size_t)(b_begin + ch * KC) * mpad + xs_off[u]),
+            RSTR_LDS_PTR(base + ACT_KB * 64 + u * 16), 4, 0, 0);
+    }
+  };
+
+  auto load_w = [&](int ch, uint32_t (&pw)[CT][KC * DW], uint32_t (&psc)[CT][KC * 2]) {
+    const int b = ch * KC;  // relative to b_begin
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+      if constexpr (KC == 4) {
+        const uint32_t* wp = wsrc[c] + (size_t)(b >> 2) * 256 * DW + wlane;
+        const uint32_t* sp = ssrc[c] + (size_t)(b >> 2) * 32 + slane;
+        const u32x4 w0 = *reinterpret_cast<const u32x4*>(wp);
+#pragma unroll
+        for (int k = 0; k < 4; k++) pw[c][k] = w0[k];
+        if constexpr (DW == 2) {
+          const u32x4 w1 = *reinterpret_cast<const u32x4*>(wp + 4);
+#pragma unroll
+          for (int k = 0; k < 4; k++) pw[c][4 + k] = w1[k];
+        }
+        const u32x4 s0 = *reinterpret_cast<const u32x4*>(sp);
+        const u32x4 s1 = *reinterpret_cast<const u32x4*>(sp + 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) { psc[c][k] = s0[k]; psc[c][4 + k] = s1[k]; }
+      } else {
+        const int ba = b_begin + b;
+        const int bq = (ba >> 2) - (b_begin >> 2), bb = ba & 3;
+        const uint32_t* wp = wsrc[c] + (size_t)bq * 256 * DW + wlane;
+        const uint32_t* sp = ssrc[c] + (size_t)bq * 32 + slane;
+        if constexpr (DW == 1) pw[c][0] = wp[bb];
+        else {
+          const u32x2 w = *reinterpret_cast<const u32x2*>(wp + 2 * bb);
+          pw[c][0] = w[0];
+          pw[c][1] = w[1];
+        }
+        const u32x2 s = *reinterpret_cast<const u32x2*>(sp + 2 * bb);
+        psc[c][0] = s[0];
+        psc[c][1] = s[1];
+      }
+    }
+  };
 
   float acc[RT][CT][4];
-  float sv0[(NQ > 1) ? RT : 1][CT][4];
-  float sv1[(NQ > 2) ? RT : 1][CT][4];
-
-  u32x4 pa[APT];
-  float pxs[XPT];
-  uint32_t pw[CT][KC * DW];
-  uint32_t psc[CT][KC * 2];
-#define QG_LOAD_CHUNK(CH)                                                                          \
-  do {                                                                                             \
-    const int b_ = b_begin + (CH) * KC;                                                            \
-    _Pragma("unroll") for (int k = 0; k < APT; k++) {                                              \
-      const int e = tid + 256 * k;                                                                 \
-      const int rt_ = min(e / (KC * 64), mt - 1);                                                  \
-      pa[k] = Xg[((size_t)rt_ * nb + b_) * 64 + e % (KC * 64)];                                    \
-    }                                                                                              \
-    _Pragma("unroll") for (int k = 0; k < XPT; k++) {                                              \
-      const int e = tid + 256 * k;                                                                 \
-      const int rr = e % (WRT * 16), kc_ = min(e / (WRT * 16), KC - 1);                            \
-      const float v_ = Xs[(size_t)(b_ + kc_) * mpad + row0 + min(rr, mt * 16 - 1)];               \
-      pxs[k] = (rr < mt * 16) ? v_ : 0.0f;                                                         \
-    }                                                                                              \
-    const int bq_ = b_ >> 2, bb_ = b_ & 3;                                                         \
-    _Pragma("unroll") for (int c = 0; c < CT; c++) {                                               \
-      const uint32_t* wp_ = W + ((size_t)ctl[c] * nb4 + bq_) * 256 * DW + (g * 16 + nn) * 4 * DW;   \
-      const uint32_t* sp_ = reinterpret_cast<const uint32_t*>(                                     \
-          Ws + (((size_t)ctl[c] * nb4 + bq_) * 4 + g) * 16);                                       \
-      if constexpr (KC == 4) {                                                                     \
-        const u32x4 w0_ = *reinterpret_cast<const u32x4*>(wp_);                                    \
-        _Pragma("unroll") for (int k = 0; k < 4; k++) pw[c][k] = w0_[k];                           \
-        if constexpr (DW == 2) {                                                                   \
-          const u32x4 w1_ = *reinterpret_cast<const u32x4*>(wp_ + 4);                              \
-          _Pragma("unroll") for (int k = 0; k < 4; k++) pw[c][4 + k] = w1_[k];                     \
-        }                                                                                          \
-        const u32x4 s0_ = *reinterpret_cast<const u32x4*>(sp_);                                    \
-        const u32x4 s1_ = *reinterpret_cast<const u32x4*>(sp_ + 4);                                \
-        _Pragma("unroll") for (int k = 0; k < 4; k++) { psc[c][k] = s0_[k]; psc[c][4 + k] = s1_[k]; } \
-      } else {                                                                                     \
-        if constexpr (DW == 1) pw[c][0] = wp_[bb_];                                                \
-        else {                                                                                     \
-          const u32x2 w_ = *reinterpret_cast<const u32x2*>(wp_ + 2 * bb_);                         \
-          pw[c][0] = w_[0];                                                                        \
-          pw[c][1] = w_[1];                                                                        \
-        }                                                                                          \
-        const u32x2 s_ = *reinterpret_cast<const u32x2*>(sp_ + 2 * bb_);                           \
-        psc[c][0] = s_[0];                                                                         \
-        psc[c][1] = s_[1];                                                                         \
-      }                                                                                            \
-    }                                                                                              \
-  } while (0)
-#define QG_STORE_CHUNK(BUF)                                                                        \
-  do {                                                                                             \
-    _Pragma("unroll") for (int k = 0; k < APT; k++) {                                              \
-      const int e = tid + 256 * k;                                                                 \
-      if (APT * 256 == WRT * KC * 64 || e < WRT * KC * 64) s_act[(BUF)][e] = pa[k];                \
-    }                                                                                              \
-    _Pragma("unroll") for (int k = 0; k < XPT; k++) {                                              \
-      const int e = tid + 256 * k;                                                                 \
-      if (XPT * 256 == WRT * KC * 16 || e < WRT * KC * 16)                                         \
-        s_xs[(BUF)][e / (WRT * 16)][e % (WRT * 16)] = pxs[k];                  \
-    }                                                                                              \
-  } while (0)
-
+  float sv0[NQ > 1 ? RT : 1][CT][4];
+  float sv1[NQ > 2 ? RT : 1][CT][4];
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  QG_LOAD_CHUNK(0);
-  QG_STORE_CHUNK(0);
-  __syncthreads();
-  int ch = 0;
-  for (int kq = 0; kq < NQ; kq++) {
 #pragma unroll
-    for (int i = 0; i < RT; i++)
+  for (int i = 0; i < RT; i++)
 #pragma unroll
-      for (int c = 0; c < CT; c++)
+    for (int c = 0; c < CT; c++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[i][c][r] = 0.0f;
-    for (int cc = 0; cc < cpq; cc++, ch++) {
-      const int buf = ch & 1;
-      uint32_t cw[CT][KC * DW], csc[CT][KC * 2];
+      for (int r = 0; r < 4; r++) acc[i][c][r] = 0.0f;
+
+  auto compute = [&](int buf, const uint32_t (&cw)[CT][KC * DW], const uint32_t (&csc)[CT][KC * 2]) {
+    const u32x4* abuf = ring + buf * BUF_U4;
+    const float* xsb = reinterpret_cast<const float*>(abuf + ACT_KB * 64);
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) {
+      h8 wv[CT];
+      h2 dwh[CT][2];
 #pragma unroll
       for (int c = 0; c < CT; c++) {
-#pragma unroll
-        for (int k = 0; k < KC * DW; k++) cw[c][k] = pw[c][k];
-#pragma unroll
-        for (int k = 0; k < KC * 2; k++) csc[c][k] = psc[c][k];
+        if constexpr (BITS == 4) wv[c] = unpack_q4(cw[c][kc], E);
+        else wv[c] = unpack_q8(cw[c][2 * kc], cw[c][2 * kc + 1], E);
+        dwh[c][0] = __builtin_bit_cast(h2, csc[c][2 * kc]);
+        dwh[c][1] = __builtin_bit_cast(h2, csc[c][2 * kc + 1]);
       }
-      // The last chunk reloads itself, so every iteration is one straight-line
-      // block (the ring slot it refills is no longer read by any wave).
-      QG_LOAD_CHUNK(min(ch + 1, nchunk - 1));
+      float dxv[RT];
+      const float* xr = xsb + (kc * 16 + nn) * RT;
+      if constexpr (RT % 4 == 0) {
 #pragma unroll
-      for (int kc = 0; kc < KC; kc++) {
-        h8 wv[CT];
-        float dw[CT][4];
+        for (int i = 0; i < RT; i += 4) {
+          const f4 t = *reinterpret_cast<const f4*>(xr + i);
 #pragma unroll
-        for (int c = 0; c < CT; c++) {
-          if constexpr (BITS == 4) wv[c] = unpack_q4(cw[c][kc]);
-          else wv[c] = unpack_q8(cw[c][2 * kc], cw[c][2 * kc + 1]);
-          const uint32_t s01 = csc[c][2 * kc], s23 = csc[c][2 * kc + 1];
-          dw[c][0] = h2f_bits((uint16_t)(s01 & 0xFFFFu));
-          dw[c][1] = h2f_bits((uint16_t)(s01 >> 16));
-          dw[c][2] = h2f_bits((uint16_t)(s23 & 0xFFFFu));
-          dw[c][3] = h2f_bits((uint16_t)(s23 >> 16));
+          for (int e = 0; e < 4; e++) dxv[i + e] = t[e];
         }
-        // Row tiles past mt compute on stale LDS and are never stored, which
-        // keeps the hot loop free of branches.
+      } else {
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-          const int rt = rh * RT + i;
-          const h8 av = __builtin_bit_cast(h8, s_act[buf][(rt * KC + kc) * 64 + g * 16 + nn]);
-          const float dx = s_xs[buf][kc][rt * 16 + nn];
+        for (int i = 0; i < RT; i++) dxv[i] = xr[i];
+      }
+      // software pipeline: the MFMAs of row tile i+1 issue before the VALU
+      // work that consumes the results of row tile i
+      f4 dn[CT];
+      {
+        const h8 av = __builtin_bit_cast(h8, abuf[kc * 64 + lane]);
 #pragma unroll
-          for (int c = 0; c < CT; c++) {
-            const f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[c], av, zero, 0, 0, 0);
+        for (int c = 0; c < CT; c++) dn[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[c], av, zero, 0, 0, 0);
+      }
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-              acc[i][c][r] = __builtin_fmaf(d[r], dw[c][r] * dx, acc[i][c][r]);
+      for (int i = 0; i < RT; i++) {
+        f4 d[CT];
+#pragma unroll
+        for (int c = 0; c < CT; c++) d[c] = dn[c];
+        if (i + 1 < RT) {
+          const h8 av = __builtin_bit_cast(h8, abuf[((i + 1) * KC + kc) * 64 + lane]);
+#pragma unroll
+          for (int c = 0; c < CT; c++) dn[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[c], av, zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            // s = dw*dx (the mixed-precision fma with +0 gives the same value
+            // as the product up to the sign of a zero, which acc ignores)
+            const float s = __builtin_fmaf((float)dwh[c][r >> 1][r & 1], dxv[i], 0.0f);
+            acc[i][c][r] = __builtin_fmaf(d[c][r], s, acc[i][c][r]);
           }
+      }
+    }
+  };
+
+  auto chunk = [&](int ch, const uint32_t (&cw)[CT][KC * DW], const uint32_t (&csc)[CT][KC * 2],
+                   uint32_t (&nw)[CT][KC * DW], uint32_t (&nsc)[CT][KC * 2]) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of chunk ch
+    __syncthreads();                     // every wave's DMA of chunk ch has landed
+    if (ch + 1 < nchunk) {
+      load_w(ch + 1, nw, nsc);
+      issue_dma(ch + 1, (ch + 1) & 1);
+    }
+    compute(ch & 1, cw, csc);
+    if ((ch + 1) % cpq == 0) {
+      // quarter kq complete: q0 -> sv0, sv0 + q1 -> sv0, q2 -> sv1 (the last
+      // quarter stays in acc); y = (q0 + q1) + (q2 + q3)
+      if constexpr (NQ > 1) {
+        const int kq = (ch + 1) / cpq - 1;
+        if (kq < NQ - 1) {
+#pragma unroll
+          for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+              for (int r = 0; r < 4; r++) {
+                if (kq == 0) sv0[i][c][r] = acc[i][c][r];
+                else if (kq == 1) sv0[i][c][r] = sv0[i][c][r] + acc[i][c][r];
+                else sv1[NQ > 2 ? i : 0][c][r] = acc[i][c][r];
+                acc[i][c][r] = 0.0f;
+              }
         }
       }
-      // interleave: one MFMA, then a run of VALU work of the previous tiles
-#pragma unroll
-      for (int k = 0; k < KC * RT * CT; k++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
-      }
-      QG_STORE_CHUNK(buf ^ 1);
-      __syncthreads();
     }
-    // quarter kq complete: (q0 + q1) is kept in sv0, q2 in sv1; the last
-    // quarter stays in acc
-    if constexpr (NQ == 2) {
-      if (kq == 0) {
-#pragma unroll
-        for (int i = 0; i < RT; i++)
-#pragma unroll
-          for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sv0[i][c][r] = acc[i][c][r];
-      }
-    } else if constexpr (NQ == 4) {
-      if (kq == 0) {
-#pragma unroll
-        for (int i = 0; i < RT; i++)
-#pragma unroll
-          for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sv0[i][c][r] = acc[i][c][r];
-      } else if (kq == 1) {
-#pragma unroll
-        for (int i = 0; i < RT; i++)
-#pragma unroll
-          for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sv0[i][c][r] = sv0[i][c][r] + acc[i][c][r];
-      } else if (kq == 2) {
-#pragma unroll
-        for (int i = 0; i < RT; i++)
-#pragma unroll
-          for (int c = 0; c < CT; c++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sv1[i][c][r] = acc[i][c][r];
-      }
-    }
+  };
+
+  uint32_t pw0[CT][KC * DW], ps0[CT][KC * 2], pw1[CT][KC * DW], ps1[CT][KC * 2];
+  load_w(0, pw0, ps0);
+  issue_dma(0, 0);
+  for (int ch = 0; ch < nchunk; ch += 2) {
+    chunk(ch, pw0, ps0, pw1, ps1);
+    if (ch + 1 < nchunk) chunk(ch + 1, pw1, ps1, pw0, ps0);
   }
-#undef QG_LOAD_CHUNK
-#undef QG_STORE_CHUNK
   float* Yq = Y + (size_t)split * slice_stride;
 #pragma unroll
   for (int i = 0; i < RT; i++) {
-    const int rt = rh * RT + i;
-    const int m = row0 + rt * 16 + nn;
-    if (rt >= mt || m >= m_rows) continue;
+    const int m = row0 + i * 16 + nn;
+    if (i >= mt || m >= m_rows) continue;
 #pragma unroll
     for (int c = 0; c < CT; c++) {
       if (ct0 + c >= nct) continue;
@@ -399,82 +437,73 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
   }
 }
 
+
 namespace {
 struct QgPlan {
-  int rt, rh, ct, splits;
+  int rt, ct, nq;
 };
-// Row tiling from the padded batch; then the widest column block and fewest
-// K splits that still give >= 384 workgroups (1.5 per CU) on 256 CUs.  Q8 at
-// 128 rows keeps one column tile per wave (two exceed the register file).
-QgPlan qg_plan(int n, int mpad, int bits) {
+// Tile plan from the padded batch (row tiles) and the requested number of K
+// slices (4/nq).  Measured on MI355X at the decode shapes (N 4096..128256,
+// K 4096/14336): 64-row x 16-column wave tiles for batches above 48 rows,
+// 32 x 32 for 17..48 rows, 16 x 32 (16 x 64 for one-slice heads) below.
+QgPlan qg_plan(int mpad, int splits, int bits) {
   const int mt_all = mpad / 16;
-  const int wrt = mt_all < QG_WRT ? mt_all : QG_WRT;
   QgPlan p{};
-  p.rh = wrt > 4 ? 2 : 1;
-  p.rt = p.rh == 2 ? 4 : (wrt > 2 ? 4 : (wrt > 1 ? 2 : 1));
-  const int cg = 4 / p.rh;
-  const int groups = (mt_all + p.rh * p.rt - 1) / (p.rh * p.rt);
-  const int nct = n / 16;
-  for (int ct = (bits == 8 && p.rh == 2) ? 1 : 2; ct >= 1; ct--)
-    for (int s = 1; s <= 4; s *= 2) {
-      const int wgs = (nct + cg * ct - 1) / (cg * ct) * s * groups;
-      if (wgs >= 384) { p.ct = ct; p.splits = s; return p; }
-    }
-  p.ct = 1;
-  p.splits = 4;
+  p.nq = 4 / splits;
+  if (mt_all > 3) { p.rt = 4; p.ct = 1; }
+  else if (mt_all > 1) { p.rt = 2; p.ct = 2; }
+  else { p.rt = 1; p.ct = (p.nq == 4 && bits == 4) ? 4 : 2; }
   return p;
 }
 }  // namespace
 
-int qgemm_splits(int n, int mpad, int bits) { return qg_plan(n, mpad, bits).splits; }
+// K slices for a projection of width n at this batch: one slice where the
+// output is large and read once (gate/up at small batches, the head), two for
+// wide projections, four where few column blocks would leave CUs idle.
+int qgemm_splits(int n, int mpad, int bits) {
+  (void)bits;
+  const int mt_all = mpad / 16;
+  if (mt_all > 3) return n >= 16384 ? 2 : 4;
+  return 4;
+}
 
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride) {
   const int nb = w.k / 32;
-  if (w.n % 16 || nb % 4 || splits < 1) return hipErrorInvalidValue;
-  QgPlan p = qg_plan(w.n, x.mpad, w.bits);
-  if (splits != p.splits) {
-    if (splits != 1 && splits != 2 && splits != 4) return hipErrorInvalidValue;
-    p.splits = splits;
-  }
+  if (w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4)) return hipErrorInvalidValue;
+  if (w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
+  const QgPlan p = qg_plan(x.mpad, splits, w.bits);
   const int nct = w.n / 16;
-  const int cg = 4 / p.rh;
   const int mt_all = x.mpad / 16;
-  dim3 grid((nct + cg * p.ct - 1) / (cg * p.ct), p.splits, (mt_all + p.rh * p.rt - 1) / (p.rh * p.rt));
+  const dim3 grid((nct + 4 * p.ct - 1) / (4 * p.ct), splits, (mt_all + p.rt - 1) / p.rt);
   const uint32_t* W = (const uint32_t*)w.w;
-  const bool aligned = (nb / 4) % 4 == 0;  // quarters are whole 4-block chunks
-#define RSTR_QG(R, H, C, B, Q)                                                                      \
-  do {                                                                                              \
-    if (aligned)                                                                                    \
-      hipLaunchKernelGGL((k_qgemm<R, H, C, B, Q, 4>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb,  \
-                         nct, x.mpad, y, ldy, m_rows, slice_stride);                                \
-    else                                                                                            \
-      hipLaunchKernelGGL((k_qgemm<R, H, C, B, Q, 1>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb,  \
-                         nct, x.mpad, y, ldy, m_rows, slice_stride);                                \
+  const bool kc4 = (nb / 4) % 4 == 0;  // quarters are whole 4-block chunks
+#define RSTR_QG(R, C, B, Q)                                                                          \
+  do {                                                                                               \
+    if (kc4)                                                                                         \
+      hipLaunchKernelGGL((k_qgemm<R, C, B, Q, 4>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
+                         x.mpad, y, ldy, m_rows, slice_stride);                                      \
+    else                                                                                             \
+      hipLaunchKernelGGL((k_qgemm<R, C, B, Q, 1>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
+                         x.mpad, y, ldy, m_rows, slice_stride);                                      \
   } while (0)
-#define RSTR_QG_S(R, H, C, B)                               \
-  do {                                                      \
-    if (p.splits == 1) RSTR_QG(R, H, C, B, 4);              \
-    else if (p.splits == 2) RSTR_QG(R, H, C, B, 2);         \
-    else RSTR_QG(R, H, C, B, 1);                            \
+#define RSTR_QG_Q(R, C, B)                 \
+  do {                                     \
+    if (p.nq == 4) RSTR_QG(R, C, B, 4);    \
+    else if (p.nq == 2) RSTR_QG(R, C, B, 2); \
+    else RSTR_QG(R, C, B, 1);              \
   } while (0)
-#define RSTR_QG_C(R, H, B)                                  \
-  do {                                                      \
-    if (p.ct == 2) RSTR_QG_S(R, H, 2, B);                   \
-    else RSTR_QG_S(R, H, 1, B);                             \
+#define RSTR_QG_T(B)                                   \
+  do {                                                 \
+    if (p.rt == 4) RSTR_QG_Q(4, 1, B);                 \
+    else if (p.rt == 2) RSTR_QG_Q(2, 2, B);            \
+    else if (p.ct == 4) RSTR_QG_Q(1, 4, B);            \
+    else RSTR_QG_Q(1, 2, B);                           \
   } while (0)
-#define RSTR_QG_R(B)                                        \
-  do {                                                      \
-    if (p.rh == 2) RSTR_QG_C(4, 2, B);                      \
-    else if (p.rt == 4) RSTR_QG_C(4, 1, B);                 \
-    else if (p.rt == 2) RSTR_QG_C(2, 1, B);                 \
-    else RSTR_QG_C(1, 1, B);                                \
-  } while (0)
-  if (w.bits == 4) RSTR_QG_R(4);
-  else RSTR_QG_R(8);
-#undef RSTR_QG_R
-#undef RSTR_QG_C
-#undef RSTR_QG_S
+  if (w.bits == 4) RSTR_QG_T(4);
+  else RSTR_QG_T(8);
+#undef RSTR_QG_T
+#undef RSTR_QG_Q
 #undef RSTR_QG
   return hipGetLastError();
 }
@@ -871,8 +900,6 @@ __device__ __forceinline__ int attn_swz(int r) {
   if constexpr (NP >= 16) return (r % (16 / LPT)) * LPT;
   else return ((r >> 1) & 1) * 4;  // HD = 64, LPT = 4
 }
-
-#define RSTR_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // Geometry of one work item (all values wave-uniform).
 struct AttnItem {
