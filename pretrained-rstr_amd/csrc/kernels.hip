@@ -1312,7 +1312,7 @@ static int attn_resident_grid(K kernel, size_t lds) {
 }
 
 // Ring depth: deeper rings keep more rows in flight per wave (fewer waves fit).
-#define RSTR_ATTN_RING 4
+#define RSTR_ATTN_RING 3
 
 template <int HD, int G, int LPT>
 static void launch_split_t(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
@@ -1341,7 +1341,7 @@ hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
     return hipGetLastError();                                                                  \
   }
   RSTR_AS(64, 1, 4) RSTR_AS(64, 2, 4) RSTR_AS(64, 4, 4) RSTR_AS(64, 8, 4)
-  RSTR_AS(128, 1, 4) RSTR_AS(128, 2, 4) RSTR_AS(128, 4, 4) RSTR_AS(128, 8, 8)
+  RSTR_AS(128, 1, 4) RSTR_AS(128, 2, 4) RSTR_AS(128, 4, 8) RSTR_AS(128, 8, 8)
   RSTR_AS(256, 1, 4) RSTR_AS(256, 2, 8) RSTR_AS(256, 4, 8) RSTR_AS(256, 8, 16)
 #undef RSTR_AS
   return hipErrorInvalidValue;
