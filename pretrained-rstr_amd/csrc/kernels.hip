@@ -508,21 +508,25 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   return hipGetLastError();
 }
 
-__device__ __forceinline__ f4 sl_load4(const Slices& s, size_t i) {
-  const f4 a = *reinterpret_cast<const f4*>(s.p + i);
-  if (s.n == 1) return a;
-  const f4 b = *reinterpret_cast<const f4*>(s.p + s.stride + i);
+// Slice sums in the canonical tree, (s0+s1) or ((s0+s1)+(s2+s3)), from loads
+// issued together.
+template <int S>
+__device__ __forceinline__ f4 sl_comb(const f4 (&v)[S]) {
+  if constexpr (S == 1) return v[0];
   f4 r;
-  if (s.n == 2) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) r[k] = a[k] + b[k];
-    return r;
+  for (int k = 0; k < 4; k++) {
+    if constexpr (S == 2) r[k] = v[0][k] + v[1][k];
+    else r[k] = (v[0][k] + v[1][k]) + (v[2][k] + v[3][k]);
   }
-  const f4 c = *reinterpret_cast<const f4*>(s.p + 2 * s.stride + i);
-  const f4 d = *reinterpret_cast<const f4*>(s.p + 3 * s.stride + i);
-#pragma unroll
-  for (int k = 0; k < 4; k++) r[k] = (a[k] + b[k]) + (c[k] + d[k]);
   return r;
+}
+template <int S>
+__device__ __forceinline__ f4 sl_get(const Slices& s, size_t i) {
+  f4 v[S];
+#pragma unroll
+  for (int k = 0; k < S; k++) v[k] = *reinterpret_cast<const f4*>(s.p + k * s.stride + i);
+  return sl_comb<S>(v);
 }
 
 // ===========================================================================
@@ -530,7 +534,9 @@ __device__ __forceinline__ f4 sl_load4(const Slices& s, size_t i) {
 // thread t owns float4 chunks c = t + 256i (elements 4c..4c+3, i.e. slot
 // (element/4) mod 256), accumulates fmaf(x,x,acc) in element order; the 256
 // slots combine by the pairwise tree (xor butterfly inside each wave, then
-// ((w0+w1)+(w2+w3)) across the four waves).
+// ((w0+w1)+(w2+w3)) across the four waves).  A thread's CPT chunks are loaded
+// together before any arithmetic, so a row costs one memory round trip per
+// phase.
 // ===========================================================================
 __device__ __forceinline__ float block_tree_sum(float v, float* sh4) {
   v = wave_tree_sum(v);
@@ -576,6 +582,7 @@ __device__ __forceinline__ void quant_store(f4 y, bool valid, int c, int row, in
   if ((c & 7) == 0) S[(size_t)b * mpad + row] = d;
 }
 
+template <int CPT>
 __global__ __launch_bounds__(256) void k_rms_quant(const float* __restrict__ x,
                                                    const float* __restrict__ g, float goff, float eps,
                                                    int n, _Float16* __restrict__ Q,
@@ -584,28 +591,45 @@ __global__ __launch_bounds__(256) void k_rms_quant(const float* __restrict__ x,
   const int tid = threadIdx.x, row = blockIdx.x;
   const float* xr = x + (size_t)row * n;
   const int n4 = n >> 2, nb = n >> 5;
-  float acc = 0.0f;
-  for (int c = tid; c < n4; c += 256) acc = fma4_sq(*reinterpret_cast<const f4*>(xr + 4 * c), acc);
-  const float r = rms_scale(block_tree_sum(acc, sh4), n, eps);
-  for (int c0 = 0; c0 < n4; c0 += 256) {
-    const int c = c0 + tid;
-    const bool valid = c < n4;
-    f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (valid) {
-      const f4 v = *reinterpret_cast<const f4*>(xr + 4 * c);
-      const f4 gg = *reinterpret_cast<const f4*>(g + 4 * c);
+  f4 xv[CPT], gg[CPT];
 #pragma unroll
-      for (int i = 0; i < 4; i++) y[i] = (v[i] * r) * (goff + gg[i]);
-    }
-    quant_store(y, valid, c, row, nb, mpad, Q, S);
+  for (int k = 0; k < CPT; k++) {
+    const int cc = min(tid + 256 * k, n4 - 1);
+    xv[k] = *reinterpret_cast<const f4*>(xr + 4 * cc);
+    gg[k] = *reinterpret_cast<const f4*>(g + 4 * cc);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPT; k++)
+    if (tid + 256 * k < n4) acc = fma4_sq(xv[k], acc);
+  const float r = rms_scale(block_tree_sum(acc, sh4), n, eps);
+#pragma unroll
+  for (int k = 0; k < CPT; k++) {
+    const int c = tid + 256 * k;
+    f4 y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = (xv[k][i] * r) * (goff + gg[k][i]);
+    quant_store(y, c < n4, c, row, nb, mpad, Q, S);
   }
 }
+
+#define RSTR_CPT_DISPATCH(N4, MACRO)          \
+  do {                                        \
+    const int cpt_ = ((N4) + 255) / 256;      \
+    if (cpt_ <= 1) MACRO(1);                  \
+    else if (cpt_ <= 2) MACRO(2);             \
+    else if (cpt_ <= 4) MACRO(4);             \
+    else if (cpt_ <= 8) MACRO(8);             \
+    else if (cpt_ <= 16) MACRO(16);           \
+    else return hipErrorInvalidValue;         \
+  } while (0)
 
 hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,
                             int rows, int n, ActBuf& out) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rms_quant, dim3(rows), dim3(256), 0, st, x, g, goff, eps, n, out.q, out.s,
-                     out.mpad);
+#define RSTR_L(C) hipLaunchKernelGGL(k_rms_quant<C>, dim3(rows), dim3(256), 0, st, x, g, goff, eps, n, out.q, out.s, out.mpad)
+  RSTR_CPT_DISPATCH(n / 4, RSTR_L);
+#undef RSTR_L
   return hipGetLastError();
 }
 
@@ -613,95 +637,129 @@ hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, floa
 // (decoder_gpu.clj layer-form: post-attn norm, residual-add!, pre-ffn norm.)
 // The same kernel serves the post-ffn step: xout = xmid + (rms(dn, pffln) | dn)
 // followed by the next layer's input norm (or the final norm of the head).
+template <int S, int CPT, bool POST>
 __global__ __launch_bounds__(256) void k_residual_norm_quant(
     Slices o, const float* __restrict__ x, float* __restrict__ xout,
     const float* __restrict__ post, const float* __restrict__ gnext, float goff, float eps, int n,
-    _Float16* __restrict__ Q, float* __restrict__ S, int mpad) {
+    _Float16* __restrict__ Q, float* __restrict__ S_, int mpad) {
   __shared__ float sh4[4];
   const int tid = threadIdx.x, row = blockIdx.x;
   const int n4 = n >> 2, nb = n >> 5;
   const size_t orow = (size_t)row * n;
-  const float* xr = x + orow;
-  float* xo = xout + orow;
-  float r1 = 1.0f;
-  if (post) {
+  f4 ov[CPT], xv[CPT], pg[POST ? CPT : 1], gg[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; k++) {
+    const int cc = min(tid + 256 * k, n4 - 1);
+    ov[k] = sl_get<S>(o, orow + 4 * cc);
+    xv[k] = *reinterpret_cast<const f4*>(x + orow + 4 * cc);
+    if constexpr (POST) pg[k] = *reinterpret_cast<const f4*>(post + 4 * cc);
+    gg[k] = *reinterpret_cast<const f4*>(gnext + 4 * cc);
+  }
+  if constexpr (POST) {
     float a = 0.0f;
-    for (int c = tid; c < n4; c += 256) a = fma4_sq(sl_load4(o, orow + 4 * c), a);
-    r1 = rms_scale(block_tree_sum(a, sh4), n, eps);
+#pragma unroll
+    for (int k = 0; k < CPT; k++)
+      if (tid + 256 * k < n4) a = fma4_sq(ov[k], a);
+    const float r1 = rms_scale(block_tree_sum(a, sh4), n, eps);
+#pragma unroll
+    for (int k = 0; k < CPT; k++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) ov[k][i] = (ov[k][i] * r1) * (goff + pg[k][i]);
   }
   float acc = 0.0f;
-  for (int c = tid; c < n4; c += 256) {
-    f4 ov = sl_load4(o, orow + 4 * c);
-    const f4 xv = *reinterpret_cast<const f4*>(xr + 4 * c);
-    if (post) {
-      const f4 pg = *reinterpret_cast<const f4*>(post + 4 * c);
+  f4 xm[CPT];
 #pragma unroll
-      for (int i = 0; i < 4; i++) ov[i] = (ov[i] * r1) * (goff + pg[i]);
+  for (int k = 0; k < CPT; k++) {
+    const int c = tid + 256 * k;
+#pragma unroll
+    for (int i = 0; i < 4; i++) xm[k][i] = xv[k][i] + ov[k][i];
+    if (c < n4) {
+      acc = fma4_sq(xm[k], acc);
+      *reinterpret_cast<f4*>(xout + orow + 4 * c) = xm[k];
     }
-    f4 xm;
-#pragma unroll
-    for (int i = 0; i < 4; i++) xm[i] = xv[i] + ov[i];
-    acc = fma4_sq(xm, acc);
-    *reinterpret_cast<f4*>(xo + 4 * c) = xm;
   }
   const float r2 = rms_scale(block_tree_sum(acc, sh4), n, eps);
-  for (int c0 = 0; c0 < n4; c0 += 256) {
-    const int c = c0 + tid;
-    const bool valid = c < n4;
-    f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (valid) {
-      const f4 v = *reinterpret_cast<const f4*>(xo + 4 * c);  // written by this thread above
-      const f4 gg = *reinterpret_cast<const f4*>(gnext + 4 * c);
 #pragma unroll
-      for (int i = 0; i < 4; i++) y[i] = (v[i] * r2) * (goff + gg[i]);
-    }
-    quant_store(y, valid, c, row, nb, mpad, Q, S);
+  for (int k = 0; k < CPT; k++) {
+    const int c = tid + 256 * k;
+    f4 y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = (xm[k][i] * r2) * (goff + gg[k][i]);
+    quant_store(y, c < n4, c, row, nb, mpad, Q, S_);
   }
+}
+
+static hipError_t launch_residual_norm(hipStream_t st, Slices o, const float* x, float* xo,
+                                       const float* post, const float* gnext, float goff, float eps,
+                                       int rows, int n, ActBuf& out) {
+  if (rows <= 0) return hipSuccess;
+#define RSTR_L3(Sn, C, P)                                                                              \
+  hipLaunchKernelGGL((k_residual_norm_quant<Sn, C, P>), dim3(rows), dim3(256), 0, st, o, x, xo, post, \
+                     gnext, goff, eps, n, out.q, out.s, out.mpad)
+#define RSTR_L2(C)                               \
+  do {                                           \
+    if (post) {                                  \
+      if (o.n == 1) RSTR_L3(1, C, true);         \
+      else if (o.n == 2) RSTR_L3(2, C, true);    \
+      else RSTR_L3(4, C, true);                  \
+    } else {                                     \
+      if (o.n == 1) RSTR_L3(1, C, false);        \
+      else if (o.n == 2) RSTR_L3(2, C, false);   \
+      else RSTR_L3(4, C, false);                 \
+    }                                            \
+  } while (0)
+  if (o.n != 1 && o.n != 2 && o.n != 4) return hipErrorInvalidValue;
+  RSTR_CPT_DISPATCH(n / 4, RSTR_L2);
+#undef RSTR_L2
+#undef RSTR_L3
+  return hipGetLastError();
 }
 
 hipError_t launch_post_attn(hipStream_t st, Slices o, const float* x, float* xmid,
                             const float* paln, const float* pfln, float goff, float eps, int rows,
                             int n, ActBuf& out) {
-  if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_residual_norm_quant, dim3(rows), dim3(256), 0, st, o, x, xmid, paln, pfln, goff,
-                     eps, n, out.q, out.s, out.mpad);
-  return hipGetLastError();
+  return launch_residual_norm(st, o, x, xmid, paln, pfln, goff, eps, rows, n, out);
 }
 
 hipError_t launch_post_ffn(hipStream_t st, Slices dn, const float* xmid, float* xout,
                            const float* pffln, const float* gnext, float goff, float eps, int rows,
                            int n, ActBuf& out) {
-  if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_residual_norm_quant, dim3(rows), dim3(256), 0, st, dn, xmid, xout, pffln, gnext,
-                     goff, eps, n, out.q, out.s, out.mpad);
-  return hipGetLastError();
+  return launch_residual_norm(st, dn, xmid, xout, pffln, gnext, goff, eps, rows, n, out);
 }
 
 // hh = act(gate) * up (gelu-mul! / silu-mul!), quantised for the down projection.
 // Element-wise with per-block quantisation: workgroups tile (row, 1024 columns).
+template <int S>
 __global__ __launch_bounds__(256) void k_act_quant(Slices gu, int ff, int geglu,
                                                    _Float16* __restrict__ Q,
-                                                   float* __restrict__ S, int mpad) {
+                                                   float* __restrict__ Sc, int mpad) {
   const int row = blockIdx.y;
   const size_t gr = (size_t)row * 2 * ff;
   const int n4 = ff >> 2, nb = ff >> 5;
   const int c = blockIdx.x * 256 + threadIdx.x;
   const bool valid = c < n4;
-  f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (valid) {
-    const f4 gv = sl_load4(gu, gr + 4 * c);
-    const f4 uv = sl_load4(gu, gr + ff + 4 * c);
+  const int cc = valid ? c : n4 - 1;
+  f4 gs[S], us[S];
 #pragma unroll
-    for (int i = 0; i < 4; i++) y[i] = (geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
+  for (int k = 0; k < S; k++) {
+    gs[k] = *reinterpret_cast<const f4*>(gu.p + k * gu.stride + gr + 4 * cc);
+    us[k] = *reinterpret_cast<const f4*>(gu.p + k * gu.stride + gr + ff + 4 * cc);
   }
-  quant_store(y, valid, c, row, nb, mpad, Q, S);
+  const f4 gv = sl_comb<S>(gs), uv = sl_comb<S>(us);
+  f4 y;
+#pragma unroll
+  for (int i = 0; i < 4; i++) y[i] = (geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
+  quant_store(y, valid, c, row, nb, mpad, Q, Sc);
 }
 
 hipError_t launch_act_quant(hipStream_t st, Slices gu, int rows, int ff, int geglu,
                             ActBuf& out) {
   if (rows <= 0) return hipSuccess;
   dim3 grid((ff / 4 + 255) / 256, rows);
-  hipLaunchKernelGGL(k_act_quant, grid, dim3(256), 0, st, gu, ff, geglu, out.q, out.s, out.mpad);
+  if (gu.n == 1) hipLaunchKernelGGL(k_act_quant<1>, grid, dim3(256), 0, st, gu, ff, geglu, out.q, out.s, out.mpad);
+  else if (gu.n == 2) hipLaunchKernelGGL(k_act_quant<2>, grid, dim3(256), 0, st, gu, ff, geglu, out.q, out.s, out.mpad);
+  else if (gu.n == 4) hipLaunchKernelGGL(k_act_quant<4>, grid, dim3(256), 0, st, gu, ff, geglu, out.q, out.s, out.mpad);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -709,7 +767,9 @@ hipError_t launch_act_quant(hipStream_t st, Slices gu, int rows, int ff, int geg
 // (HF rotate-half: y_i = x_i c - x_{i+h} s, y_{i+h} = x_{i+h} c + x_i s),
 // then q -> qr (f32), k -> fp16 page slot, v -> fp16 page slot (slot -1 skips).
 // (decoder_gpu.clj layer-form steps qk-norm, rope-pos-rows-buf!, and the
-// routed append of paged_append.clj:179-228.)
+// routed append of paged_append.clj:179-228.)  head_dim <= 256, so lane l
+// holds chunk l (elements 4l..4l+3) of the head.
+template <int S>
 __global__ __launch_bounds__(64) void k_qkv_post(Slices y, int n_q, int n_kv,
                                                  int hd, const float* __restrict__ qn,
                                                  const float* __restrict__ kn, float goff, float eps,
@@ -720,34 +780,35 @@ __global__ __launch_bounds__(64) void k_qkv_post(Slices y, int n_q, int n_kv,
                                                  float* __restrict__ qr, uint16_t* __restrict__ kp,
                                                  uint16_t* __restrict__ vp) {
   __shared__ float sh[256];
-  int nh = n_q + 2 * n_kv;
-  int row = blockIdx.x / nh, hh = blockIdx.x % nh;
-  int lane = threadIdx.x;
-  int qd = n_q * hd, kvr = n_kv * hd, ncols = qd + 2 * kvr;
+  const int nh = n_q + 2 * n_kv;
+  const int row = blockIdx.x / nh, hh = blockIdx.x % nh;
+  const int lane = threadIdx.x;
+  const int qd = n_q * hd, kvr = n_kv * hd, ncols = qd + 2 * kvr;
   const size_t yr = (size_t)row * ncols;
-  int slot = slots[row];
-  int hd4 = hd >> 2;
+  const int slot = slots[row];
+  const int hd4 = hd >> 2;
+  const bool have = lane < hd4;
+  const int cc = have ? lane : 0;
   if (hh >= n_q + n_kv) {
     if (slot < 0) return;
-    int j = hh - n_q - n_kv;
-    const size_t src = yr + qd + kvr + j * hd;
-    uint16_t* dst = vp + (size_t)slot * kvr + j * hd;
-    for (int c = lane; c < hd4; c += 64) {
-      f4 v = sl_load4(y, src + 4 * c);
+    const int j = hh - n_q - n_kv;
+    const f4 v = sl_get<S>(y, yr + qd + kvr + j * hd + 4 * cc);
+    if (have) {
+      uint16_t* dst = vp + (size_t)slot * kvr + j * hd;
 #pragma unroll
-      for (int i = 0; i < 4; i++) dst[4 * c + i] = f2h_bits(v[i]);
+      for (int i = 0; i < 4; i++) dst[4 * lane + i] = f2h_bits(v[i]);
     }
     return;
   }
-  bool is_q = hh < n_q;
+  const bool is_q = hh < n_q;
   if (!is_q && slot < 0) return;
   const size_t src = is_q ? yr + hh * hd : yr + qd + (hh - n_q) * hd;
   const float* gn = is_q ? qn : kn;
-  float r = 1.0f;
+  f4 v = sl_get<S>(y, src + 4 * cc);
   if (gn) {
+    const f4 gg = *reinterpret_cast<const f4*>(gn + 4 * cc);
     float a = 0.0f;
-    for (int c = lane; c < hd4; c += 64) {
-      f4 v = sl_load4(y, src + 4 * c);
+    if (have) {
       a = __builtin_fmaf(v[0], v[0], a);
       a = __builtin_fmaf(v[1], v[1], a);
       a = __builtin_fmaf(v[2], v[2], a);
@@ -755,21 +816,17 @@ __global__ __launch_bounds__(64) void k_qkv_post(Slices y, int n_q, int n_kv,
     }
     // head_dim/4 <= 64 chunks: lane l holds slot l alone, and the tree over
     // 64 lanes equals the 256-slot tree (the other slots are +0).
-    r = rms_scale(wave_tree_sum(a), hd, eps);
+    const float r = rms_scale(wave_tree_sum(a), hd, eps);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = (v[i] * r) * (goff + gg[i]);
   }
-  for (int c = lane; c < hd4; c += 64) {
-    f4 v = sl_load4(y, src + 4 * c);
-    if (gn) {
-      f4 gg = *reinterpret_cast<const f4*>(gn + 4 * c);
+  if (have) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = (v[i] * r) * (goff + gg[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) sh[4 * c + i] = v[i];
+    for (int i = 0; i < 4; i++) sh[4 * lane + i] = v[i];
   }
   __syncthreads();
-  int half = hd >> 1;
-  int pos = positions[row];
+  const int half = hd >> 1;
+  const int pos = positions[row];
   const float* ct = cos_t + (size_t)pos * half;
   const float* stt = sin_t + (size_t)pos * half;
   for (int i = lane; i < half; i += 64) {
@@ -792,9 +849,16 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
                            const float* qn, const float* kn, float goff, float eps,
                            const float* cos_t, const float* sin_t, const int32_t* positions,
                            const int32_t* slots, float* qr, uint16_t* kpages, uint16_t* vpages) {
-  int nh = n_q + 2 * n_kv;
-  hipLaunchKernelGGL(k_qkv_post, dim3(rows * nh), dim3(64), 0, st, yqkv, n_q, n_kv, hd, qn, kn, goff,
-                     eps, cos_t, sin_t, positions, slots, qr, kpages, vpages);
+  if (hd > 256 || hd % 4) return hipErrorInvalidValue;
+  const int nh = n_q + 2 * n_kv;
+#define RSTR_L(Sn)                                                                                       \
+  hipLaunchKernelGGL(k_qkv_post<Sn>, dim3(rows * nh), dim3(64), 0, st, yqkv, n_q, n_kv, hd, qn, kn, goff, \
+                     eps, cos_t, sin_t, positions, slots, qr, kpages, vpages)
+  if (yqkv.n == 1) RSTR_L(1);
+  else if (yqkv.n == 2) RSTR_L(2);
+  else if (yqkv.n == 4) RSTR_L(4);
+  else return hipErrorInvalidValue;
+#undef RSTR_L
   return hipGetLastError();
 }
 
@@ -1376,12 +1440,26 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
       M = fmaxf(M, part[(size_t)(base + kk) * stride + hl * (HD + 2) + HD]);
     M = wave_max(M);
     float L = 0.0f;
-    for (int kk = 0; kk < ns; kk++) {
-      const float* pr = part + (size_t)(base + kk) * stride + hl * (HD + 2);
-      const float w = dexp(pr[HD] - M);
-      L = __builtin_fmaf(pr[HD + 1], w, L);
+    // splits in order, their partials loaded 8 at a time
+    for (int k0 = 0; k0 < ns; k0 += 8) {
+      float mk[8], lk[8], ok[8][DPL];
 #pragma unroll
-      for (int d = 0; d < DPL; d++) O[d] = __builtin_fmaf(pr[lane * DPL + d], w, O[d]);
+      for (int j = 0; j < 8; j++) {
+        const float* pr = part + (size_t)(base + min(k0 + j, ns - 1)) * stride + hl * (HD + 2);
+        mk[j] = pr[HD];
+        lk[j] = pr[HD + 1];
+#pragma unroll
+        for (int d = 0; d < DPL; d++) ok[j][d] = pr[lane * DPL + d];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        if (k0 + j < ns) {
+          const float w = dexp(mk[j] - M);
+          L = __builtin_fmaf(lk[j], w, L);
+#pragma unroll
+          for (int d = 0; d < DPL; d++) O[d] = __builtin_fmaf(ok[j][d], w, O[d]);
+        }
+      }
     }
 #pragma unroll
     for (int d = 0; d < DPL; d++) O[d] = O[d] / L;
