@@ -871,34 +871,59 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
 // (visible tokens of the split) + RSTR_ITEM_OVH; cbase is the cost prefix the
 // split kernel partitions into equal shares, one per resident wave.
 #define RSTR_ITEM_OVH 16
-__global__ void k_attn_prep(int batch, int split, int window, int n_kv,
-                            const int32_t* __restrict__ lengths, int32_t* __restrict__ tab) {
-  // tab: lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]
-  if (threadIdx.x != 0) return;
+__global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int window, int n_kv,
+                                                   const int32_t* __restrict__ lengths,
+                                                   int32_t* __restrict__ tab) {
+  // tab: lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]; base and cbase are
+  // exclusive prefix sums over lanes (integer sums: any order is exact)
+  __shared__ int32_t s_a[1024], s_c[1024];
   int32_t* lo = tab;
   int32_t* k0 = tab + batch;
   int32_t* ns = tab + 2 * batch;
   int32_t* base = tab + 3 * batch;
   int32_t* cbase = tab + 4 * batch + 1;
-  int32_t acc = 0, cacc = 0;
-  for (int b = 0; b < batch; b++) {
-    int len = lengths[b];
-    int l0 = 0, kk0 = 0, n = 0;
-    if (len > 0) {
-      l0 = window > 0 ? max(0, len - window) : 0;
-      kk0 = l0 / split;
-      n = (len - 1) / split - kk0 + 1;
+  const int tid = threadIdx.x;
+  int32_t carry_a = 0, carry_c = 0;
+  for (int b0 = 0; b0 < batch; b0 += 1024) {
+    const int b = b0 + tid;
+    int l0 = 0, kk0 = 0, n = 0, len = 0;
+    if (b < batch) {
+      len = lengths[b];
+      if (len > 0) {
+        l0 = window > 0 ? max(0, len - window) : 0;
+        kk0 = l0 / split;
+        n = (len - 1) / split - kk0 + 1;
+      }
+      lo[b] = l0;
+      k0[b] = kk0;
+      ns[b] = n;
     }
-    lo[b] = l0;
-    k0[b] = kk0;
-    ns[b] = n;
-    base[b] = acc;
-    cbase[b] = cacc;
-    acc += n * n_kv;
-    cacc += n_kv * ((len - l0) + n * RSTR_ITEM_OVH);
+    const int32_t va = b < batch ? n * n_kv : 0;
+    const int32_t vc = b < batch ? n_kv * ((len - l0) + n * RSTR_ITEM_OVH) : 0;
+    // inclusive Hillis-Steele scan over the 1024 lanes of this chunk
+    s_a[tid] = va;
+    s_c[tid] = vc;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int32_t ta = tid >= off ? s_a[tid - off] : 0;
+      const int32_t tc = tid >= off ? s_c[tid - off] : 0;
+      __syncthreads();
+      s_a[tid] += ta;
+      s_c[tid] += tc;
+      __syncthreads();
+    }
+    if (b < batch) {
+      base[b] = carry_a + s_a[tid] - va;
+      cbase[b] = carry_c + s_c[tid] - vc;
+    }
+    carry_a += s_a[1023];
+    carry_c += s_c[1023];
+    __syncthreads();
   }
-  base[batch] = acc;
-  cbase[batch] = cacc;
+  if (tid == 0) {
+    base[batch] = carry_a;
+    cbase[batch] = carry_c;
+  }
 }
 
 // First item whose starting cost is >= x (items in (lane, kv head, split)
@@ -939,7 +964,7 @@ __device__ __forceinline__ int attn_first_item(int x, int batch, int n_kv, int s
 
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                             int32_t* lane_tab) {
-  hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(64), 0, st, g.batch, g.split, g.window, g.n_kv,
+  hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv,
                      lengths, lane_tab);
   return hipGetLastError();
 }
@@ -1537,9 +1562,30 @@ __global__ __launch_bounds__(1024) void k_argmax_gather(const float* __restrict_
   const float* lr = logits + (size_t)row * vocab;
   float bv = 0.0f;
   int bi = INT_MAX;
-  for (int i = tid; i < vocab; i += 1024) {
-    const float v = lr[i];
-    if (arg_take(bv, bi, v, i)) { bv = v; bi = i; }
+  if ((vocab & 3) == 0) {
+    // float4 chunks, eight loads in flight per thread (the winner does not
+    // depend on the order in which candidates are compared)
+    const int n4 = vocab >> 2;
+    const f4* l4 = reinterpret_cast<const f4*>(lr);
+    for (int c0 = tid; c0 < n4; c0 += 8 * 1024) {
+      f4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = l4[min(c0 + j * 1024, n4 - 1)];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int c = c0 + j * 1024;
+        if (c < n4) {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (arg_take(bv, bi, v[j][e], 4 * c + e)) { bv = v[j][e]; bi = 4 * c + e; }
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < vocab; i += 1024) {
+      const float v = lr[i];
+      if (arg_take(bv, bi, v, i)) { bv = v; bi = i; }
+    }
   }
   sv[tid] = bv;
   si[tid] = bi;
