@@ -1387,9 +1387,9 @@ static int attn_resident_grid(K kernel, size_t lds) {
   static int per_cu = 0;
   if (cus == 0) {
     int dev = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (cus <= 0) cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
   }
   if (cached_lds != lds || per_cu == 0) {
     int n = 0;
