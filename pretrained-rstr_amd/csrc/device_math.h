@@ -105,6 +105,12 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __shfl_xor(v, M, 64);
 }
 
+// v[lane'] where lane' mirrors lane inside its aligned 8-lane group
+// (i -> 7 - i): one DPP row_half_mirror.
+__device__ __forceinline__ float half_mirror_lane(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+}
+
 // xor butterfly: level m combines lanes i and i^m.  Because fp add commutes,
 // both lanes hold the same value and the result is the balanced pairwise tree
 // over lane order.

@@ -20,6 +20,7 @@
 //   (the routed-append ABI of doc/serving-architecture.md:178-190).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace rstr {
@@ -76,12 +77,25 @@ struct AttnGeom {
   int batch, n_q, n_kv, hd, page_size, pps, split, window;
   float scale;
 };
+// Attention work table of one step and window geometry (int32 words):
+//   lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]   per lane (window start, first
+//       split, split count, item prefix, cost prefix);
+//   wave[R+1]                                    first item of each resident
+//       wave of the split kernel (R = attn_grid);
+//   items[max_items][4] at a 16-byte boundary    (lane, kv head, t0, t1).
+// max_items bounds the step's items (sum over lanes of n_kv * splits).
+inline int lane_tab_words(int batch) { return 5 * batch + 2; }
+inline size_t attn_items_offset(int batch, int R) {
+  return ((size_t)lane_tab_words(batch) + R + 1 + 3) & ~(size_t)3;
+}
+int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported geometry
+size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
-                            int32_t* lane_tab);
+                            int32_t* lane_tab, int max_items);
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
-                             const int32_t* page_table, const int32_t* lengths,
-                             const int32_t* lane_tab, float* part, int max_items);
+                             const int32_t* page_table, const int32_t* lane_tab, float* part,
+                             int max_items);
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                              int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q);
@@ -102,8 +116,5 @@ hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
                                  int64_t page_elems, const uint16_t* tmpl, const int32_t* pages,
                                  int npages, uint64_t seed);
 
-// lane table layout (int32): lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]; cbase
-// is the prefix of item costs that the split kernel divides between waves.
-inline int lane_tab_words(int batch) { return 5 * batch + 2; }
 
 }  // namespace rstr

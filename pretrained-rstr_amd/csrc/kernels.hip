@@ -7,6 +7,7 @@
 #include "device_math.h"
 #include "kernels.h"
 
+#include <algorithm>
 #include <climits>
 
 namespace rstr {
@@ -962,10 +963,51 @@ __device__ __forceinline__ int attn_first_item(int x, int batch, int n_kv, int s
   return base[b] + h * ns + idx;
 }
 
+// The step's flattened work: item i = (lane, kv head, t0, t1) in (lane, kv
+// head, split) order, and the first item of each of the R resident waves of
+// the split kernel (wave w takes the items whose starting cost lies in
+// [w*C/R, (w+1)*C/R)).  Built once per step, read by every layer.
+__global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int split, int R,
+                                                    const int32_t* __restrict__ lengths,
+                                                    int32_t* __restrict__ tab,
+                                                    int32_t* __restrict__ wave, int4* __restrict__ items) {
+  const int32_t* lo_t = tab;
+  const int32_t* k0_t = tab + batch;
+  const int32_t* ns_t = tab + 2 * batch;
+  const int32_t* base = tab + 3 * batch;
+  const int32_t* cbase = tab + 4 * batch + 1;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < base[batch]) {
+    // the last lane whose first item is <= i (lanes without items have
+    // base[b] == base[b+1], so the search lands on the lane that holds i)
+    int lo = 0, hi = batch;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (base[mid] <= i) lo = mid; else hi = mid;
+    }
+    const int ns = ns_t[lo];
+    const int rel = i - base[lo];
+    const int kvh = rel / ns;
+    const int k = k0_t[lo] + rel % ns;
+    items[i] = int4{lo, kvh, max(lo_t[lo], k * split), min(lengths[lo], (k + 1) * split)};
+  }
+  if (i <= R) {
+    const int64_t ctot = cbase[batch];
+    wave[i] = attn_first_item((int)(ctot * i / R), batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase,
+                              lengths);
+  }
+}
+
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
-                            int32_t* lane_tab) {
+                            int32_t* lane_tab, int max_items) {
+  const int R = attn_grid(g, max_items);
+  if (R <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv,
                      lengths, lane_tab);
+  const int n = std::max(max_items, R + 1);
+  hipLaunchKernelGGL(k_attn_items, dim3((n + 255) / 256), dim3(256), 0, st, g.batch, g.n_kv, g.split, R,
+                     lengths, lane_tab, lane_tab + lane_tab_words(g.batch),
+                     reinterpret_cast<int4*>(lane_tab + attn_items_offset(g.batch, R)));
   return hipGetLastError();
 }
 
@@ -1000,67 +1042,27 @@ struct AttnItem {
 // compiler wait for every outstanding DMA).
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__device__ __forceinline__ void attn_item_fill(AttnItem& it, int split,
-                                               const int32_t* __restrict__ lo_t,
-                                               const int32_t* __restrict__ k0_t,
-                                               const int32_t* __restrict__ lengths) {
-  it.b = uni(it.b);
-  it.kvh = uni(it.kvh);
-  it.idx = uni(it.idx);
-  const int k = uni(k0_t[it.b]) + it.idx;
-  it.t0 = uni(max(lo_t[it.b], k * split));
-  it.t1 = uni(min(lengths[it.b], (k + 1) * split));
-  it.T0 = it.t0 & ~15;
-  it.nch = (it.t1 - it.T0 + 15) / 16;
-}
-
-// The item after `it` in (lane, kv head, split) order (lanes without
-// visible tokens hold no items).  Callers stop at their range end, so the
-// lane index never runs past the last lane that holds items.
-__device__ __forceinline__ void attn_item_next(AttnItem& it, int batch, int n_kv, int split,
-                                               const int32_t* __restrict__ lo_t,
-                                               const int32_t* __restrict__ k0_t,
-                                               const int32_t* __restrict__ ns_t,
-                                               const int32_t* __restrict__ lengths) {
-  int b = uni(it.b);
-  if (++it.idx >= uni(ns_t[b])) {
-    it.idx = 0;
-    if (++it.kvh >= n_kv) {
-      it.kvh = 0;
-      do { b = uni(b + 1); } while (b < batch - 1 && uni(ns_t[b]) == 0);
-    }
-  }
-  it.b = b;
-  attn_item_fill(it, split, lo_t, k0_t, lengths);
-}
-
-__device__ __forceinline__ AttnItem attn_item(int item, int batch, int split,
-                                              const int32_t* __restrict__ lo_t,
-                                              const int32_t* __restrict__ k0_t,
-                                              const int32_t* __restrict__ ns_t,
-                                              const int32_t* __restrict__ base,
-                                              const int32_t* __restrict__ lengths) {
-  int lo = 0, hi = batch;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (base[mid] <= item) lo = mid; else hi = mid;
-  }
+// Item i of the step's flattened item table: (lane, kv head, t0, t1).  The
+// index is wave-uniform, so this is one scalar load.
+__device__ __forceinline__ AttnItem attn_item_at(const int4* __restrict__ items, int i) {
+  const int4 d = items[i];
   AttnItem it;
-  it.b = lo;
-  const int ns = ns_t[lo];
-  const int rel = item - base[lo];
-  it.kvh = rel / ns;
-  it.idx = rel % ns;
-  attn_item_fill(it, split, lo_t, k0_t, lengths);
+  it.b = uni(d.x);
+  it.kvh = uni(d.y);
+  it.idx = 0;
+  it.t0 = uni(d.z);
+  it.t1 = uni(d.w);
+  it.T0 = it.t0 & ~15;
+  it.nch = (it.t1 - it.T0 + 15) >> 4;
   return it;
 }
 
 template <int HD, int G, int LPT, bool PG16, int RB>
 __global__ __launch_bounds__(64) void k_attn_split(
-    int batch, int n_kv, int page_size, int pps, int split, float scale,
+    int n_kv, int page_size, int pps, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
-    const int32_t* __restrict__ page_table, const int32_t* __restrict__ lengths,
-    const int32_t* __restrict__ tab, float* __restrict__ part) {
+    const int32_t* __restrict__ page_table, const int32_t* __restrict__ wave_tab,
+    const int4* __restrict__ items, float* __restrict__ part) {
   constexpr int NP = HD / 8;             // 16-byte pieces per row
   constexpr int CT = 16;                 // tokens per chunk
   constexpr int CU16 = CT * NP;          // 16-byte units per chunk
@@ -1077,13 +1079,16 @@ __global__ __launch_bounds__(64) void k_attn_split(
   u32x4* qlds = ring + RB * CU16;                                       // [QB][64]
   float* sc = reinterpret_cast<float*>(qlds + QB * 64);                 // [split][G]
   const int lane = threadIdx.x;
-  const int32_t* lo_t = tab;
-  const int32_t* k0_t = tab + batch;
-  const int32_t* ns_t = tab + 2 * batch;
-  const int32_t* base = tab + 3 * batch;
-  const int32_t* cbase = tab + 4 * batch + 1;
   const int kvr = n_kv * HD;
   const int ts = lane / LPT, j = lane % LPT;
+  // Lane j of a token's LPT lanes owns 8-dim chunks jp + LPT*i.  For LPT = 8
+  // the order 0 1 2 3 7 6 5 4 puts slices s and s^4 in mirrored lanes of the
+  // 8-lane group, so the bit-2 merge is one DPP half-row mirror (bits 1 and 0
+  // stay quad permutes); for other LPT, jp = j.
+  const int jp = (LPT == 8 && j >= 4) ? 11 - j : j;
+  static_assert(CT % TPP == 0, "a QK pass covers a whole number of chunk rows");
+  constexpr int NPASS = CT / TPP;            // QK passes per chunk
+  constexpr int QPB = NPASS >= 2 ? 2 : 1;    // passes per batch
   const int grp = lane >> 4, e16 = lane & 15;
   // per-lane DMA geometry: row within the chunk and element offset of the
   // lane's 16-byte piece for each of the chunk's LPC load instructions
@@ -1097,20 +1102,19 @@ __global__ __launch_bounds__(64) void k_attn_split(
     dma_boff[u] = (uint32_t)(dma_r[u] * kvr + dma_off[u]) * 2u;
   }
 
-  // Static cost-balanced partition: wave w takes the items whose starting
-  // cost lies in [w*C/R, (w+1)*C/R), a contiguous run of items.
-  const int64_t ctot = cbase[batch];
-  const int x0 = (int)(ctot * blockIdx.x / gridDim.x);
-  const int x1 = (int)(ctot * (blockIdx.x + 1) / gridDim.x);
-  const int i_begin = attn_first_item(x0, batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase, lengths);
-  const int i_end = attn_first_item(x1, batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase, lengths);
+  // Static cost-balanced partition (built once per step): wave w takes the
+  // contiguous item run [wave_tab[w], wave_tab[w+1]).
+  const int i_begin = uni(wave_tab[blockIdx.x]);
+  const int i_end = uni(wave_tab[blockIdx.x + 1]);
   if (i_begin >= i_end) return;
 
   // One continuous stream per wave: the positions of item i are its K
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
   // consumer across item boundaries, so the ring never drains between items.
   int pi = i_begin, ppos = 0;  // producer cursor
-  AttnItem gp = attn_item(pi, batch, split, lo_t, k0_t, ns_t, base, lengths);
+  AttnItem gp = attn_item_at(items, pi);
+  AttnItem gpn = attn_item_at(items, min(pi + 1, i_end - 1));  // the next item, loaded one item early
+  AttnItem gc = gp, gcn = gpn;  // the consumer's item and its successor
   int issued = 0;
   // page of the producer's next chunk (one page per chunk when page_size % 16 == 0)
   int pg_next = 0;
@@ -1141,7 +1145,10 @@ __global__ __launch_bounds__(64) void k_attn_split(
     issued++;                                                                                     \
     if (++ppos == 2 * gp.nch) {                                                                   \
       ppos = 0;                                                                                   \
-      if (++pi < i_end) attn_item_next(gp, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);         \
+      if (++pi < i_end) {                                                                         \
+        gp = gpn;                                                                                 \
+        gpn = attn_item_at(items, min(pi + 1, i_end - 1));                                        \
+      }                                                                                           \
     }                                                                                             \
     if constexpr (PG16) {                                                                         \
       if (pi < i_end) {                                                                           \
@@ -1156,7 +1163,6 @@ __global__ __launch_bounds__(64) void k_attn_split(
 
   // consumer
   int ci = i_begin, cpos = 0, consumed = 0;
-  AttnItem gc = attn_item(i_begin, batch, split, lo_t, k0_t, ns_t, base, lengths);
   float qv[G][NCL][8];
   // A kv group's G query rows are contiguous: they reach LDS by QB DMA
   // instructions (lanes past the end re-read the last piece).
@@ -1174,7 +1180,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
     const float* qf_ = reinterpret_cast<const float*>(qlds);                                      \
     _Pragma("unroll") for (int h = 0; h < G; h++)                                                 \
       _Pragma("unroll") for (int i = 0; i < NCL; i++) {                                           \
-        const int cch = j + LPT * i;                                                              \
+        const int cch = jp + LPT * i;                                                             \
         const f4 a = *reinterpret_cast<const f4*>(qf_ + h * HD + 8 * cch);                        \
         const f4 bq = *reinterpret_cast<const f4*>(qf_ + h * HD + 8 * cch + 4);                   \
         _Pragma("unroll") for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = bq[e]; } \
@@ -1209,50 +1215,67 @@ __global__ __launch_bounds__(64) void k_attn_split(
     const int t0 = gc.t0, t1 = gc.t1;
     if (cpos < gc.nch) {
       // ---- QK over the 16 rows of this chunk --------------------------------
+      // Passes run in batches of QPB: every LDS read of a batch is issued
+      // before its fmas, and the cross-lane merges of the batch's G*QPB dots
+      // are independent DPP operations.
 #pragma unroll
-      for (int pass = 0; pass < CT / TPP + (CT % TPP ? 1 : 0); pass++) {
-        const int r = pass * TPP + ts;
-        const int t = gc.T0 + cpos * CT + r;
-        const bool valid = r < CT && t >= t0 && t < t1;
-        const int rr = r < CT ? r : CT - 1;
-        float sv[G][NSL];
+      for (int pb = 0; pb < NPASS; pb += QPB) {
+        float sv[QPB][G][NSL];
 #pragma unroll
-        for (int h = 0; h < G; h++)
-#pragma unroll
-          for (int u = 0; u < NSL; u++) sv[h][u] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NCL; i++) {
-          const int piece = j + LPT * i;
-          const h8 kv = __builtin_bit_cast(h8, buf[rr * NP + (piece ^ attn_swz<HD, LPT>(rr))]);
+        for (int ps = 0; ps < QPB; ps++)
 #pragma unroll
           for (int h = 0; h < G; h++)
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-              sv[h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[e], sv[h][i % NSL]);
+            for (int u = 0; u < NSL; u++) sv[ps][h][u] = 0.0f;
+        h8 kv[QPB][NCL];
+#pragma unroll
+        for (int ps = 0; ps < QPB; ps++) {
+          const int r = (pb + ps) * TPP + ts;
+#pragma unroll
+          for (int i = 0; i < NCL; i++) {
+            const int piece = jp + LPT * i;
+            kv[ps][i] = __builtin_bit_cast(h8, buf[r * NP + (piece ^ attn_swz<HD, LPT>(r))]);
+          }
         }
-        float scv[G];
 #pragma unroll
-        for (int h = 0; h < G; h++) {
-          float v;
-          if constexpr (LPT == 4) v = (sv[h][0] + sv[h][2]) + (sv[h][1] + sv[h][3]);
-          else if constexpr (LPT == 8) v = sv[h][0] + sv[h][1];
-          else v = sv[h][0];
-          if constexpr (LPT >= 16) v = v + xor_lane<8>(v);
-          if constexpr (LPT >= 8) v = v + xor_lane<4>(v);
-          v = v + xor_lane<2>(v);
-          v = v + xor_lane<1>(v);
-          scv[h] = v * scale;
-          if (valid) mx[h] = fmaxf(mx[h], scv[h]);
-        }
-        if (valid && j == 0) {
-          float* dst = sc + (size_t)(t - t0) * G;
-          if constexpr (G % 4 == 0) {
+        for (int ps = 0; ps < QPB; ps++)
 #pragma unroll
-            for (int h4 = 0; h4 < G; h4 += 4)
-              *reinterpret_cast<f4*>(dst + h4) = f4{scv[h4], scv[h4 + 1], scv[h4 + 2], scv[h4 + 3]};
-          } else {
+          for (int i = 0; i < NCL; i++)
 #pragma unroll
-            for (int h = 0; h < G; h++) dst[h] = scv[h];
+            for (int h = 0; h < G; h++)
+#pragma unroll
+              for (int e = 0; e < 8; e++)
+                sv[ps][h][i % NSL] = __builtin_fmaf(qv[h][i][e], (float)kv[ps][i][e], sv[ps][h][i % NSL]);
+#pragma unroll
+        for (int ps = 0; ps < QPB; ps++) {
+          const int r = (pb + ps) * TPP + ts;
+          const int t = gc.T0 + cpos * CT + r;
+          const bool valid = t >= t0 && t < t1;
+          float scv[G];
+#pragma unroll
+          for (int h = 0; h < G; h++) {
+            float v;
+            if constexpr (LPT == 4) v = (sv[ps][h][0] + sv[ps][h][2]) + (sv[ps][h][1] + sv[ps][h][3]);
+            else if constexpr (LPT == 8) v = sv[ps][h][0] + sv[ps][h][1];
+            else v = sv[ps][h][0];
+            if constexpr (LPT >= 16) v = v + xor_lane<8>(v);
+            if constexpr (LPT == 8) v = v + half_mirror_lane(v);  // slices jp and jp ^ 4
+            else if constexpr (LPT >= 16) v = v + xor_lane<4>(v);
+            v = v + xor_lane<2>(v);
+            v = v + xor_lane<1>(v);
+            scv[h] = v * scale;
+            if (valid) mx[h] = fmaxf(mx[h], scv[h]);
+          }
+          if (valid && j == 0) {
+            float* dst = sc + (size_t)(t - t0) * G;
+            if constexpr (G % 4 == 0) {
+#pragma unroll
+              for (int h4 = 0; h4 < G; h4 += 4)
+                *reinterpret_cast<f4*>(dst + h4) = f4{scv[h4], scv[h4 + 1], scv[h4 + 2], scv[h4 + 3]};
+            } else {
+#pragma unroll
+              for (int h = 0; h < G; h++) dst[h] = scv[h];
+            }
           }
         }
       }
@@ -1272,9 +1295,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
         // the next item's query: its DMA lands while this item's V chunks run
         // (qv itself is reloaded from LDS when the next item starts)
         if (ci + 1 < i_end) {
-          AttnItem gn = gc;
-          attn_item_next(gn, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);
-          RSTR_ATTN_DMA_Q(gn);
+          RSTR_ATTN_DMA_Q(gcn);
           q_dma_step = consumed;
         }
       }
@@ -1360,7 +1381,8 @@ __global__ __launch_bounds__(64) void k_attn_split(
     }
     if (++ci >= i_end) break;
     cpos = 0;
-    attn_item_next(gc, batch, n_kv, split, lo_t, k0_t, ns_t, lengths);
+    gc = gcn;
+    gcn = attn_item_at(items, min(ci + 1, i_end - 1));
     // the query DMA is complete once a position issued after it has been
     // waited for; position p is issued at consumer step p - (RB - 1)
     if (consumed - 1 < q_dma_step + RB) __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1379,60 +1401,88 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #undef RSTR_ATTN_READ_Q
 }
 
-// Resident workgroups per CU of one split-kernel instantiation (cached).
-template <typename K>
-static int attn_resident_grid(K kernel, size_t lds) {
-  static int cus = 0;
-  static size_t cached_lds = 0;
-  static int per_cu = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
-  if (cached_lds != lds || per_cu == 0) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64, lds) != hipSuccess || n <= 0) n = 2;
-    per_cu = n;
-    cached_lds = lds;
-  }
-  return cus * per_cu;
-}
-
 // Ring depth: deeper rings keep more rows in flight per wave (fewer waves fit).
 #define RSTR_ATTN_RING 3
 
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+// One split-kernel instantiation: its LDS bytes and its resident grid (one
+// wave per workgroup, every wave resident, never more waves than items).
 template <int HD, int G, int LPT>
-static void launch_split_t(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
-                           const uint16_t* vp, const int32_t* pt, const int32_t* len,
-                           const int32_t* tab, float* part, int max_items) {
-  constexpr int RB = RSTR_ATTN_RING;
-  size_t lds = (size_t)RB * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
-               sizeof(float) * G * g.split;
-  auto kern = (g.page_size % 16 == 0) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
-  int grid = attn_resident_grid(kern, lds);
-  if (grid > max_items) grid = max_items;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64), lds, st, g.batch, g.n_kv, g.page_size, g.pps, g.split,
-                     g.scale, q, kp, vp, pt, len, tab, part);
+struct AttnSplit {
+  static constexpr int RB = RSTR_ATTN_RING;
+  static size_t lds(const AttnGeom& g) {
+    return (size_t)RB * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
+           sizeof(float) * G * g.split;
+  }
+  static decltype(&k_attn_split<HD, G, LPT, true, RB>) kernel(const AttnGeom& g) {
+    return (g.page_size % 16 == 0) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
+  }
+  static int grid(const AttnGeom& g, int max_items) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel(g), 64, lds(g)) != hipSuccess || n <= 0) n = 2;
+    return std::max(1, std::min(device_cus() * n, max_items));
+  }
+  static void launch(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
+                     const uint16_t* vp, const int32_t* pt, const int32_t* tab, float* part,
+                     int max_items) {
+    const int R = grid(g, max_items);
+    const int32_t* wave = tab + lane_tab_words(g.batch);
+    const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch, R));
+    hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, g.pps, g.scale, q, kp,
+                       vp, pt, wave, items, part);
+  }
+};
+
+// Dispatch over the supported (head dim, GQA group) pairs with their QK lane
+// counts; OP(HD, G, LPT) must return.
+#define RSTR_ATTN_DISPATCH(g, OP)                                                          \
+  do {                                                                                     \
+    const int G_ = (g).n_q / (g).n_kv;                                                     \
+    if ((g).hd == 64 && G_ == 1) OP(64, 1, 4);                                             \
+    if ((g).hd == 64 && G_ == 2) OP(64, 2, 4);                                             \
+    if ((g).hd == 64 && G_ == 4) OP(64, 4, 4);                                             \
+    if ((g).hd == 64 && G_ == 8) OP(64, 8, 4);                                             \
+    if ((g).hd == 128 && G_ == 1) OP(128, 1, 4);                                           \
+    if ((g).hd == 128 && G_ == 2) OP(128, 2, 4);                                           \
+    if ((g).hd == 128 && G_ == 4) OP(128, 4, 8);                                           \
+    if ((g).hd == 128 && G_ == 8) OP(128, 8, 8);                                           \
+    if ((g).hd == 256 && G_ == 1) OP(256, 1, 4);                                           \
+    if ((g).hd == 256 && G_ == 2) OP(256, 2, 8);                                           \
+    if ((g).hd == 256 && G_ == 4) OP(256, 4, 8);                                           \
+    if ((g).hd == 256 && G_ == 8) OP(256, 8, 16);                                          \
+  } while (0)
+
+int attn_grid(const AttnGeom& g, int max_items) {
+#define RSTR_AG(HD_, G_, L_) return AttnSplit<HD_, G_, L_>::grid(g, max_items)
+  RSTR_ATTN_DISPATCH(g, RSTR_AG);
+#undef RSTR_AG
+  return 0;
+}
+
+size_t attn_tab_words(const AttnGeom& g, int max_items) {
+  const int R = attn_grid(g, max_items);
+  if (R <= 0) return 0;
+  return attn_items_offset(g.batch, R) + (size_t)4 * max_items;
 }
 
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
-                             const int32_t* page_table, const int32_t* lengths,
-                             const int32_t* lane_tab, float* part, int max_items) {
-  int G = g.n_q / g.n_kv;
-#define RSTR_AS(HD_, G_, L_)                                                                   \
-  if (g.hd == HD_ && G == G_) {                                                                \
-    launch_split_t<HD_, G_, L_>(st, g, q, kpages, vpages, page_table, lengths, lane_tab, part, \
-                                max_items);                                                    \
-    return hipGetLastError();                                                                  \
+                             const int32_t* page_table, const int32_t* lane_tab, float* part,
+                             int max_items) {
+#define RSTR_AL(HD_, G_, L_)                                                                            \
+  {                                                                                                     \
+    AttnSplit<HD_, G_, L_>::launch(st, g, q, kpages, vpages, page_table, lane_tab, part, max_items); \
+    return hipGetLastError();                                                                           \
   }
-  RSTR_AS(64, 1, 4) RSTR_AS(64, 2, 4) RSTR_AS(64, 4, 4) RSTR_AS(64, 8, 4)
-  RSTR_AS(128, 1, 4) RSTR_AS(128, 2, 4) RSTR_AS(128, 4, 8) RSTR_AS(128, 8, 8)
-  RSTR_AS(256, 1, 4) RSTR_AS(256, 2, 8) RSTR_AS(256, 4, 8) RSTR_AS(256, 8, 16)
-#undef RSTR_AS
+  RSTR_ATTN_DISPATCH(g, RSTR_AL);
+#undef RSTR_AL
   return hipErrorInvalidValue;
 }
 

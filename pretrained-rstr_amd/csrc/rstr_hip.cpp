@@ -135,7 +135,8 @@ struct rstr_decoder {
   float *rope_cos = nullptr, *rope_sin = nullptr;   // [2][maxpos][hd/2]
   ActBuf act;
   int32_t* desc = nullptr;                          // device descriptors
-  int32_t* lane_tab = nullptr;                      // [2][4B+1]
+  int32_t* lane_tab = nullptr;                      // [2][tabw] attention work tables
+  size_t tabw = 0;                                  // words per work table
   int32_t* tokbuf = nullptr;
   int32_t *d_lanes = nullptr, *d_tokens = nullptr;  // priming staging
   // pinned host staging
@@ -723,7 +724,10 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   A(dmalloc(&d->act.q, (size_t)d->mpad * d->kmax));
   A(dmalloc(&d->act.s, (size_t)d->mpad * (d->kmax / 32)));
   A(dmalloc(&d->desc, (size_t)d->desc_words));
-  A(dmalloc(&d->lane_tab, (size_t)2 * lane_tab_words(batch)));
+  d->tabw = attn_tab_words(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps, split, 0,
+                                     md.attn_scale}, d->max_items);
+  if (d->tabw == 0 && e == hipSuccess) e = hipErrorInvalidValue;
+  A(dmalloc(&d->lane_tab, 2 * d->tabw));
   A(dmalloc(&d->tokbuf, (size_t)batch));
   A(dmalloc(&d->d_lanes, (size_t)batch));
   A(dmalloc(&d->d_tokens, (size_t)batch));
@@ -933,9 +937,10 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
     geo[w] = AttnGeom{B, md.n_q, md.n_kv, hd, d->p->page_size, d->pps, d->split,
                       w == 1 ? md.sliding_window : 0, md.attn_scale};
   }
-  const int tabw = lane_tab_words(B);
-  run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[0], len, d->lane_tab); });
-  if (has_window) run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[1], len, d->lane_tab + tabw); });
+  const size_t tabw = d->tabw;
+  run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[0], len, d->lane_tab, d->max_items); });
+  if (has_window)
+    run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[1], len, d->lane_tab + tabw, d->max_items); });
   run(RSTR_K_ROWS, [&] {
     return launch_rms_quant(st, d->r0, d->m->layers[0].attn_norm, goff, md.eps, B, dm, d->act);
   });
@@ -956,8 +961,7 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
                              d->rope_sin + (size_t)ti * d->maxpos * half, pos, slots, d->qr, kp, vp);
     });
     run(RSTR_K_ATTN_SPLIT, [&] {
-      return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, len, d->lane_tab + wi * tabw, d->part,
-                               d->max_items);
+      return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
     });
     run(RSTR_K_ATTN_MERGE, [&] {
       return launch_attn_merge(st, geo[wi], len, d->lane_tab + wi * tabw, d->part, nullptr, &d->act);
@@ -1288,11 +1292,13 @@ static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q,
   HIPCHK(s, dmalloc(&bf.part, (size_t)*max_items * G * (hd + 2)));
   HIPCHK(s, dmalloc(&bf.pt, (size_t)batch * pps));
   HIPCHK(s, dmalloc(&bf.len, (size_t)batch));
-  HIPCHK(s, dmalloc(&bf.tab, (size_t)lane_tab_words(batch)));
+  geo = AttnGeom{batch, n_q, md.n_kv, hd, ps, pps, split, window, 0.0f};
+  const size_t tabw = attn_tab_words(geo, *max_items);
+  if (tabw == 0) return fail(s, RSTR_E_INVALID, "unsupported attention geometry");
+  HIPCHK(s, dmalloc(&bf.tab, tabw));
   HIPCHK(s, hipMemcpy(bf.q, q, sizeof(float) * batch * n_q * hd, hipMemcpyHostToDevice));
   HIPCHK(s, hipMemcpy(bf.pt, pt, sizeof(int32_t) * batch * pps, hipMemcpyHostToDevice));
   HIPCHK(s, hipMemcpy(bf.len, len, sizeof(int32_t) * batch, hipMemcpyHostToDevice));
-  geo = AttnGeom{batch, n_q, md.n_kv, hd, ps, pps, split, window, 0.0f};
   return RSTR_OK;
 }
 
@@ -1317,9 +1323,9 @@ extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, in
   geo.scale = scale;
   hipStream_t st = s->stream;
   int L = p->m->d.n_layers;
-  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab));
-  HIPCHK(s, launch_attn_split(st, geo, bf.q, p->slabs[layer], p->slabs[L + layer], bf.pt, bf.len, bf.tab,
-                              bf.part, max_items));
+  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab, max_items));
+  HIPCHK(s, launch_attn_split(st, geo, bf.q, p->slabs[layer], p->slabs[L + layer], bf.pt, bf.tab, bf.part,
+                              max_items));
   HIPCHK(s, launch_attn_merge(st, geo, bf.len, bf.tab, bf.part, bf.out, nullptr));
   HIPCHK(s, hipStreamSynchronize(st));
   HIPCHK(s, hipMemcpy(out, bf.out, sizeof(float) * batch * n_q * geo.hd, hipMemcpyDeviceToHost));
@@ -1341,13 +1347,13 @@ extern "C" int rstr_attention_bench(rstr_pool* p, int32_t layer, int32_t batch, 
   geo.scale = scale;
   hipStream_t st = s->stream;
   int L = p->m->d.n_layers;
-  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab));
+  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab, max_items));
   std::vector<hipEvent_t> ev(4 * iters);
   for (auto& e : ev) HIPCHK(s, hipEventCreate(&e));
   for (int i = 0; i < iters; i++) {
     HIPCHK(s, hipEventRecord(ev[4 * i], st));
-    HIPCHK(s, launch_attn_split(st, geo, bf.q, p->slabs[layer], p->slabs[L + layer], bf.pt, bf.len, bf.tab,
-                                bf.part, max_items));
+    HIPCHK(s, launch_attn_split(st, geo, bf.q, p->slabs[layer], p->slabs[L + layer], bf.pt, bf.tab, bf.part,
+                                max_items));
     HIPCHK(s, hipEventRecord(ev[4 * i + 1], st));
     HIPCHK(s, hipEventRecord(ev[4 * i + 2], st));
     HIPCHK(s, launch_attn_merge(st, geo, bf.len, bf.tab, bf.part, bf.out, nullptr));

@@ -200,7 +200,7 @@ def test_append_rejects_duplicate_slots(sess):
 # ---------------------------------------------------------------------------
 # attention vs the oracle on random ragged inputs
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (256, 4, 1), (64, 8, 2), (128, 16, 8)])
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (256, 4, 1), (64, 8, 2), (128, 16, 8), (128, 4, 1)])
 @pytest.mark.parametrize("split,window", [(256, 0), (32, 0), (16, 24)])
 def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
     print(f"case attention hd{hd} q{n_q} kv{n_kv} split{split} window{window}", flush=True)
