@@ -1043,9 +1043,10 @@ struct AttnItem {
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Item i of the step's flattened item table: (lane, kv head, t0, t1).  The
-// index is wave-uniform, so this is one scalar load.
-__device__ __forceinline__ AttnItem attn_item_at(const int4* __restrict__ items, int i) {
-  const int4 d = items[i];
+// index is wave-uniform, so this is one scalar load.  Prefetched items stay
+// raw until used, so no wait is placed at the load.
+__device__ __forceinline__ int4 attn_item_raw(const int4* __restrict__ items, int i) { return items[i]; }
+__device__ __forceinline__ AttnItem attn_item_make(int4 d) {
   AttnItem it;
   it.b = uni(d.x);
   it.kvh = uni(d.y);
@@ -1059,7 +1060,7 @@ __device__ __forceinline__ AttnItem attn_item_at(const int4* __restrict__ items,
 
 template <int HD, int G, int LPT, bool PG16, int RB>
 __global__ __launch_bounds__(64) void k_attn_split(
-    int n_kv, int page_size, int pps, float scale,
+    int n_kv, int page_size, int ps_shift, int pps, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ wave_tab,
     const int4* __restrict__ items, float* __restrict__ part) {
@@ -1112,24 +1113,28 @@ __global__ __launch_bounds__(64) void k_attn_split(
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
   // consumer across item boundaries, so the ring never drains between items.
   int pi = i_begin, ppos = 0;  // producer cursor
-  AttnItem gp = attn_item_at(items, pi);
-  AttnItem gpn = attn_item_at(items, min(pi + 1, i_end - 1));  // the next item, loaded one item early
-  AttnItem gc = gp, gcn = gpn;  // the consumer's item and its successor
-  int issued = 0;
-  // page of the producer's next chunk (one page per chunk when page_size % 16 == 0)
+  AttnItem gp = attn_item_make(attn_item_raw(items, pi));
+  int4 gpn = attn_item_raw(items, min(pi + 1, i_end - 1));  // the next item, loaded one item early
+  AttnItem gc = gp;                                          // the consumer's item
+  int4 gcn = gpn;                                            // and its successor
+  int pslot = 0;  // ring slot of the producer's next chunk
+  // PG16: page_size is a power of two and a multiple of 16, so a chunk lies in
+  // one page; pg_next is the page of the producer's next chunk.
+  const uint32_t row_bytes = (uint32_t)kvr * 2u;
+  const uint32_t page_bytes = (uint32_t)page_size * row_bytes;
   int pg_next = 0;
-  if constexpr (PG16) pg_next = page_table[(size_t)gp.b * pps + gp.T0 / page_size];
+  if constexpr (PG16) pg_next = page_table[(size_t)gp.b * pps + (gp.T0 >> ps_shift)];
 
 #define RSTR_ATTN_ISSUE()                                                                         \
   do {                                                                                            \
     const bool isk_ = ppos < gp.nch;                                                              \
     const int c_ = isk_ ? ppos : ppos - gp.nch;                                                   \
     const uint16_t* src_ = (isk_ ? kp : vp) + gp.kvh * HD;                                        \
-    u32x4* dst_ = ring + (issued % RB) * CU16;                                                    \
+    u32x4* dst_ = ring + pslot * CU16;                                                            \
     const int tb_ = gp.T0 + c_ * CT;                                                              \
     if constexpr (PG16) {                                                                         \
-      const char* cb_ = reinterpret_cast<const char*>(                                            \
-          src_ + ((size_t)pg_next * page_size + (tb_ % page_size)) * kvr);                        \
+      const char* cb_ = reinterpret_cast<const char*>(src_) + (uint64_t)(uint32_t)pg_next * page_bytes + \
+                        (uint32_t)(tb_ & (page_size - 1)) * row_bytes;                            \
       _Pragma("unroll") for (int u = 0; u < LPC; u++)                                             \
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(cb_ + dma_boff[u]),        \
                                          RSTR_LDS_PTR(dst_ + u * 64), 16, 0, 0);                  \
@@ -1142,18 +1147,18 @@ __global__ __launch_bounds__(64) void k_attn_split(
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g_), RSTR_LDS_PTR(dst_ + u * 64), 16, 0, 0); \
       }                                                                                           \
     }                                                                                             \
-    issued++;                                                                                     \
+    pslot = pslot == RB - 1 ? 0 : pslot + 1;                                                      \
     if (++ppos == 2 * gp.nch) {                                                                   \
       ppos = 0;                                                                                   \
       if (++pi < i_end) {                                                                         \
-        gp = gpn;                                                                                 \
-        gpn = attn_item_at(items, min(pi + 1, i_end - 1));                                        \
+        gp = attn_item_make(gpn);                                                                 \
+        gpn = attn_item_raw(items, min(pi + 1, i_end - 1));                                       \
       }                                                                                           \
     }                                                                                             \
     if constexpr (PG16) {                                                                         \
       if (pi < i_end) {                                                                           \
         const int cn_ = ppos < gp.nch ? ppos : ppos - gp.nch;                                     \
-        pg_next = page_table[(size_t)gp.b * pps + (gp.T0 + cn_ * CT) / page_size];                \
+        pg_next = page_table[(size_t)gp.b * pps + ((gp.T0 + cn_ * CT) >> ps_shift)];              \
       }                                                                                           \
     }                                                                                             \
   } while (0)
@@ -1162,7 +1167,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
     if (pi < i_end) RSTR_ATTN_ISSUE();
 
   // consumer
-  int ci = i_begin, cpos = 0, consumed = 0;
+  int ci = i_begin, cpos = 0, consumed = 0, cslot = 0;
   float qv[G][NCL][8];
   // A kv group's G query rows are contiguous: they reach LDS by QB DMA
   // instructions (lanes past the end re-read the last piece).
@@ -1211,7 +1216,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stream is draining
     }
     __asm__ __volatile__("" ::: "memory");
-    const u32x4* buf = ring + (consumed % RB) * CU16;
+    const u32x4* buf = ring + cslot * CU16;
     const int t0 = gc.t0, t1 = gc.t1;
     if (cpos < gc.nch) {
       // ---- QK over the 16 rows of this chunk --------------------------------
@@ -1295,7 +1300,8 @@ __global__ __launch_bounds__(64) void k_attn_split(
         // the next item's query: its DMA lands while this item's V chunks run
         // (qv itself is reloaded from LDS when the next item starts)
         if (ci + 1 < i_end) {
-          RSTR_ATTN_DMA_Q(gcn);
+          const AttnItem gn = attn_item_make(gcn);
+          RSTR_ATTN_DMA_Q(gn);
           q_dma_step = consumed;
         }
       }
@@ -1348,6 +1354,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #undef RSTR_PV_ROUNDS
     }
     consumed++;
+    cslot = cslot == RB - 1 ? 0 : cslot + 1;
     if (++cpos < 2 * gc.nch) continue;
     // ---- item complete: combine lane groups, write the partial ---------------
 #pragma unroll
@@ -1381,8 +1388,8 @@ __global__ __launch_bounds__(64) void k_attn_split(
     }
     if (++ci >= i_end) break;
     cpos = 0;
-    gc = gcn;
-    gcn = attn_item_at(items, min(ci + 1, i_end - 1));
+    gc = attn_item_make(gcn);
+    gcn = attn_item_raw(items, min(ci + 1, i_end - 1));
     // the query DMA is complete once a position issued after it has been
     // waited for; position p is issued at consumer step p - (RB - 1)
     if (consumed - 1 < q_dma_step + RB) __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1421,8 +1428,10 @@ struct AttnSplit {
     return (size_t)RB * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
            sizeof(float) * G * g.split;
   }
+  // whole-page chunks: page_size a power of two and a multiple of 16
+  static bool pg16(const AttnGeom& g) { return g.page_size % 16 == 0 && (g.page_size & (g.page_size - 1)) == 0; }
   static decltype(&k_attn_split<HD, G, LPT, true, RB>) kernel(const AttnGeom& g) {
-    return (g.page_size % 16 == 0) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
+    return pg16(g) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
   }
   static int grid(const AttnGeom& g, int max_items) {
     int n = 0;
@@ -1435,8 +1444,9 @@ struct AttnSplit {
     const int R = grid(g, max_items);
     const int32_t* wave = tab + lane_tab_words(g.batch);
     const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch, R));
-    hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, g.pps, g.scale, q, kp,
-                       vp, pt, wave, items, part);
+    const int shift = pg16(g) ? __builtin_ctz((unsigned)g.page_size) : 0;
+    hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
+                       kp, vp, pt, wave, items, part);
   }
 };
 
