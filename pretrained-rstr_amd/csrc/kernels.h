@@ -78,16 +78,14 @@ struct AttnGeom {
   float scale;
 };
 // Attention work table of one step and window geometry (int32 words):
-//   lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]   per lane (window start, first
-//       split, split count, item prefix, cost prefix);
-//   wave[R+1]                                    first item of each resident
-//       wave of the split kernel (R = attn_grid);
-//   items[max_items][4] at a 16-byte boundary    (lane, kv head, t0, t1).
+//   lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]   per lane (window
+//       start, first split, split count, and prefixes of its items, full
+//       items and partial items);
+//   items[max_items][4] at a 16-byte boundary: the work list, full items then
+//       partial ones, entries (lane | kv head << 20, t0, t1, item index).
 // max_items bounds the step's items (sum over lanes of n_kv * splits).
-inline int lane_tab_words(int batch) { return 5 * batch + 2; }
-inline size_t attn_items_offset(int batch, int R) {
-  return ((size_t)lane_tab_words(batch) + R + 1 + 3) & ~(size_t)3;
-}
+inline int lane_tab_words(int batch) { return 6 * batch + 3; }
+inline size_t attn_items_offset(int batch) { return ((size_t)lane_tab_words(batch) + 3) & ~(size_t)3; }
 int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported geometry
 size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,

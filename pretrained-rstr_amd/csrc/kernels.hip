@@ -868,146 +868,128 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
 // Work item = (lane, kv head, history split of `split` tokens); items are
 // packed by a device-side lane table so ragged lanes cost only their pages.
 // ===========================================================================
-// Per-lane item table.  Item (lane b, kv head h, split k) has cost
-// (visible tokens of the split) + RSTR_ITEM_OVH; cbase is the cost prefix the
-// split kernel partitions into equal shares, one per resident wave.
-#define RSTR_ITEM_OVH 16
+// Per-lane item table.  Item (lane b, kv head h, split k) covers the visible
+// tokens [max(lo, k*split), min(len, (k+1)*split)).  A split is full when it
+// holds `split` tokens; only a lane's first (window start) and last split can
+// be partial.
 __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int window, int n_kv,
                                                    const int32_t* __restrict__ lengths,
                                                    int32_t* __restrict__ tab) {
-  // tab: lo[B] k0[B] nsplit[B] base[B+1] cbase[B+1]; base and cbase are
-  // exclusive prefix sums over lanes (integer sums: any order is exact)
-  __shared__ int32_t s_a[1024], s_c[1024];
+  // tab: lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]; base, fbase
+  // and pbase are exclusive prefix sums over lanes of the lane's items, full
+  // items and partial items (integer sums: any order is exact)
+  __shared__ int32_t s_a[1024], s_f[1024], s_p[1024];
   int32_t* lo = tab;
   int32_t* k0 = tab + batch;
   int32_t* ns = tab + 2 * batch;
   int32_t* base = tab + 3 * batch;
-  int32_t* cbase = tab + 4 * batch + 1;
+  int32_t* fbase = tab + 4 * batch + 1;
+  int32_t* pbase = tab + 5 * batch + 2;
   const int tid = threadIdx.x;
-  int32_t carry_a = 0, carry_c = 0;
+  int32_t carry_a = 0, carry_f = 0, carry_p = 0;
   for (int b0 = 0; b0 < batch; b0 += 1024) {
     const int b = b0 + tid;
-    int l0 = 0, kk0 = 0, n = 0, len = 0;
+    int l0 = 0, kk0 = 0, n = 0, f = 0;
     if (b < batch) {
-      len = lengths[b];
+      const int len = lengths[b];
       if (len > 0) {
         l0 = window > 0 ? max(0, len - window) : 0;
         kk0 = l0 / split;
         n = (len - 1) / split - kk0 + 1;
+        const bool first_full = l0 == kk0 * split && min(len, (kk0 + 1) * split) - l0 == split;
+        const bool last_full = len % split == 0;
+        f = n == 1 ? (first_full ? 1 : 0) : n - (first_full ? 0 : 1) - (last_full ? 0 : 1);
       }
       lo[b] = l0;
       k0[b] = kk0;
       ns[b] = n;
     }
     const int32_t va = b < batch ? n * n_kv : 0;
-    const int32_t vc = b < batch ? n_kv * ((len - l0) + n * RSTR_ITEM_OVH) : 0;
-    // inclusive Hillis-Steele scan over the 1024 lanes of this chunk
+    const int32_t vf = b < batch ? f * n_kv : 0;
+    const int32_t vp = va - vf;
+    // inclusive Hillis-Steele scans over the 1024 lanes of this chunk
     s_a[tid] = va;
-    s_c[tid] = vc;
+    s_f[tid] = vf;
+    s_p[tid] = vp;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {
       const int32_t ta = tid >= off ? s_a[tid - off] : 0;
-      const int32_t tc = tid >= off ? s_c[tid - off] : 0;
+      const int32_t tf = tid >= off ? s_f[tid - off] : 0;
+      const int32_t tp = tid >= off ? s_p[tid - off] : 0;
       __syncthreads();
       s_a[tid] += ta;
-      s_c[tid] += tc;
+      s_f[tid] += tf;
+      s_p[tid] += tp;
       __syncthreads();
     }
     if (b < batch) {
       base[b] = carry_a + s_a[tid] - va;
-      cbase[b] = carry_c + s_c[tid] - vc;
+      fbase[b] = carry_f + s_f[tid] - vf;
+      pbase[b] = carry_p + s_p[tid] - vp;
     }
     carry_a += s_a[1023];
-    carry_c += s_c[1023];
+    carry_f += s_f[1023];
+    carry_p += s_p[1023];
     __syncthreads();
   }
   if (tid == 0) {
     base[batch] = carry_a;
-    cbase[batch] = carry_c;
+    fbase[batch] = carry_f;
+    pbase[batch] = carry_p;
   }
 }
 
-// First item whose starting cost is >= x (items in (lane, kv head, split)
-// order; within one kv head of lane b the splits cost tok0+OVH, then
-// split+OVH each, the last one possibly less).
-__device__ __forceinline__ int attn_first_item(int x, int batch, int n_kv, int split,
-                                               const int32_t* __restrict__ lo_t,
-                                               const int32_t* __restrict__ k0_t,
-                                               const int32_t* __restrict__ ns_t,
-                                               const int32_t* __restrict__ base,
-                                               const int32_t* __restrict__ cbase,
-                                               const int32_t* __restrict__ lengths) {
-  if (x >= cbase[batch]) return base[batch];
-  int lo = 0, hi = batch;  // last lane with cbase <= x
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (cbase[mid] <= x) lo = mid; else hi = mid;
-  }
-  int b = lo;
-  while (b < batch && ns_t[b] == 0) b++;  // empty lanes own no cost
-  if (b >= batch) return base[batch];
-  const int ns = ns_t[b];
-  const int len = lengths[b];
-  const int l0 = lo_t[b];
-  const int kc = (len - l0) + ns * RSTR_ITEM_OVH;  // cost of one kv head's splits
-  const int rel = max(0, x - cbase[b]);
-  int h = rel / kc;
-  const int r2 = rel - h * kc;
-  const int c0 = min(len, (k0_t[b] + 1) * split) - l0 + RSTR_ITEM_OVH;  // first split
-  int idx;
-  if (r2 <= 0) idx = 0;
-  else if (r2 <= c0) idx = 1;
-  else idx = 1 + (r2 - c0 + split + RSTR_ITEM_OVH - 1) / (split + RSTR_ITEM_OVH);
-  if (idx >= ns) { idx = 0; h++; }
-  if (h >= n_kv) return base[b + 1];
-  return base[b] + h * ns + idx;
-}
-
-// The step's flattened work: item i = (lane, kv head, t0, t1) in (lane, kv
-// head, split) order, and the first item of each of the R resident waves of
-// the split kernel (wave w takes the items whose starting cost lies in
-// [w*C/R, (w+1)*C/R)).  Built once per step, read by every layer.
-__global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int split, int R,
+// The step's work list: every item once, full items first (in (lane, kv
+// head, split) order), then the partial ones.  Wave w of the R resident waves
+// takes list positions k*R + w for even rounds k and k*R + R-1-w for odd ones
+// (a snake), so waves hold equal counts of full items and the partial ones
+// even out the remainder.  Entry = (lane | kv head << 20, t0, t1, item index).
+// Built once per step, read by every layer.
+__global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int split,
                                                     const int32_t* __restrict__ lengths,
-                                                    int32_t* __restrict__ tab,
-                                                    int32_t* __restrict__ wave, int4* __restrict__ items) {
+                                                    const int32_t* __restrict__ tab,
+                                                    int4* __restrict__ items) {
   const int32_t* lo_t = tab;
   const int32_t* k0_t = tab + batch;
   const int32_t* ns_t = tab + 2 * batch;
   const int32_t* base = tab + 3 * batch;
-  const int32_t* cbase = tab + 4 * batch + 1;
+  const int32_t* fbase = tab + 4 * batch + 1;
+  const int32_t* pbase = tab + 5 * batch + 2;
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < base[batch]) {
-    // the last lane whose first item is <= i (lanes without items have
-    // base[b] == base[b+1], so the search lands on the lane that holds i)
-    int lo = 0, hi = batch;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (base[mid] <= i) lo = mid; else hi = mid;
-    }
-    const int ns = ns_t[lo];
-    const int rel = i - base[lo];
-    const int kvh = rel / ns;
-    const int k = k0_t[lo] + rel % ns;
-    items[i] = int4{lo, kvh, max(lo_t[lo], k * split), min(lengths[lo], (k + 1) * split)};
+  if (i >= base[batch]) return;
+  // the last lane whose first item is <= i (lanes without items have
+  // base[b] == base[b+1], so the search lands on the lane that holds i)
+  int b = 0, hi = batch;
+  while (hi - b > 1) {
+    const int mid = (b + hi) >> 1;
+    if (base[mid] <= i) b = mid; else hi = mid;
   }
-  if (i <= R) {
-    const int64_t ctot = cbase[batch];
-    wave[i] = attn_first_item((int)(ctot * i / R), batch, n_kv, split, lo_t, k0_t, ns_t, base, cbase,
-                              lengths);
-  }
+  const int ns = ns_t[b];
+  const int rel = i - base[b];
+  const int kvh = rel / ns;
+  const int s = rel % ns;
+  const int len = lengths[b];
+  const int k = k0_t[b] + s;
+  const int t0 = max(lo_t[b], k * split), t1 = min(len, (k + 1) * split);
+  const int nf = (fbase[b + 1] - fbase[b]) / n_kv;  // full splits of this lane
+  const int l0 = lo_t[b];
+  const bool first_partial = !(l0 == k0_t[b] * split && min(len, (k0_t[b] + 1) * split) - l0 == split);
+  const int before = (first_partial && s > 0) ? 1 : 0;  // partial splits ahead of s
+  int pos;
+  if (t1 - t0 == split) pos = fbase[b] + kvh * nf + (s - before);
+  else pos = fbase[batch] + pbase[b] + kvh * (ns - nf) + before;
+  items[pos] = int4{b | (kvh << 20), t0, t1, i};
 }
 
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                             int32_t* lane_tab, int max_items) {
   const int R = attn_grid(g, max_items);
   if (R <= 0) return hipErrorInvalidValue;
+  if (g.batch >= (1 << 20) || g.n_kv >= (1 << 11)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv,
                      lengths, lane_tab);
-  const int n = std::max(max_items, R + 1);
-  hipLaunchKernelGGL(k_attn_items, dim3((n + 255) / 256), dim3(256), 0, st, g.batch, g.n_kv, g.split, R,
-                     lengths, lane_tab, lane_tab + lane_tab_words(g.batch),
-                     reinterpret_cast<int4*>(lane_tab + attn_items_offset(g.batch, R)));
+  hipLaunchKernelGGL(k_attn_items, dim3((max_items + 255) / 256), dim3(256), 0, st, g.batch, g.n_kv, g.split,
+                     lengths, lane_tab, reinterpret_cast<int4*>(lane_tab + attn_items_offset(g.batch)));
   return hipGetLastError();
 }
 
@@ -1042,17 +1024,21 @@ struct AttnItem {
 // compiler wait for every outstanding DMA).
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Item i of the step's flattened item table: (lane, kv head, t0, t1).  The
-// index is wave-uniform, so this is one scalar load.  Prefetched items stay
-// raw until used, so no wait is placed at the load.
-__device__ __forceinline__ int4 attn_item_raw(const int4* __restrict__ items, int i) { return items[i]; }
+// Round k of this wave's share of the step's work list (positions k*R + w,
+// then k*R + R-1-w, alternating).  The position is wave-uniform, so this is
+// one scalar load.  Prefetched entries stay raw until used, so no wait is
+// placed at the load.
+__device__ __forceinline__ int4 attn_item_raw(const int4* __restrict__ items, int k) {
+  const int R = gridDim.x, w = blockIdx.x;
+  return items[(size_t)k * R + ((k & 1) ? R - 1 - w : w)];
+}
 __device__ __forceinline__ AttnItem attn_item_make(int4 d) {
   AttnItem it;
-  it.b = uni(d.x);
-  it.kvh = uni(d.y);
-  it.idx = 0;
-  it.t0 = uni(d.z);
-  it.t1 = uni(d.w);
+  it.b = uni(d.x & 0xFFFFF);
+  it.kvh = uni(d.x >> 20);
+  it.idx = uni(d.w);
+  it.t0 = uni(d.y);
+  it.t1 = uni(d.z);
   it.T0 = it.t0 & ~15;
   it.nch = (it.t1 - it.T0 + 15) >> 4;
   return it;
@@ -1062,7 +1048,7 @@ template <int HD, int G, int LPT, bool PG16, int RB>
 __global__ __launch_bounds__(64) void k_attn_split(
     int n_kv, int page_size, int ps_shift, int pps, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
-    const int32_t* __restrict__ page_table, const int32_t* __restrict__ wave_tab,
+    const int32_t* __restrict__ page_table, const int32_t* __restrict__ n_items,
     const int4* __restrict__ items, float* __restrict__ part) {
   constexpr int NP = HD / 8;             // 16-byte pieces per row
   constexpr int CT = 16;                 // tokens per chunk
@@ -1103,11 +1089,16 @@ __global__ __launch_bounds__(64) void k_attn_split(
     dma_boff[u] = (uint32_t)(dma_r[u] * kvr + dma_off[u]) * 2u;
   }
 
-  // Static cost-balanced partition (built once per step): wave w takes the
-  // contiguous item run [wave_tab[w], wave_tab[w+1]).
-  const int i_begin = uni(wave_tab[blockIdx.x]);
-  const int i_end = uni(wave_tab[blockIdx.x + 1]);
-  if (i_begin >= i_end) return;
+  // This wave's rounds of the work list: every wave takes N / R full rounds,
+  // and the last round's first N % R positions go to the waves that own them.
+  const int i_begin = 0;
+  int i_end;
+  {
+    const int N = uni(*n_items), R = gridDim.x, w = blockIdx.x;
+    const int kq = N / R, kr = N % R;
+    i_end = kq + ((((kq & 1) ? R - 1 - w : w) < kr) ? 1 : 0);
+  }
+  if (i_end <= 0) return;
 
   // One continuous stream per wave: the positions of item i are its K
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
@@ -1367,7 +1358,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
         o[h][d] = o[h][d] + xor_lane<32>(o[h][d]);
       }
     }
-    float* prt = part + (size_t)ci * G * (HD + 2);
+    float* prt = part + (size_t)gc.idx * G * (HD + 2);
     if (grp == 0) {
 #pragma unroll
       for (int h = 0; h < G; h++) {
@@ -1442,11 +1433,11 @@ struct AttnSplit {
                      const uint16_t* vp, const int32_t* pt, const int32_t* tab, float* part,
                      int max_items) {
     const int R = grid(g, max_items);
-    const int32_t* wave = tab + lane_tab_words(g.batch);
-    const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch, R));
+    const int32_t* n_items = tab + 4 * g.batch;  // base[batch]
+    const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch));
     const int shift = pg16(g) ? __builtin_ctz((unsigned)g.page_size) : 0;
     hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
-                       kp, vp, pt, wave, items, part);
+                       kp, vp, pt, n_items, items, part);
   }
 };
 
@@ -1477,9 +1468,8 @@ int attn_grid(const AttnGeom& g, int max_items) {
 }
 
 size_t attn_tab_words(const AttnGeom& g, int max_items) {
-  const int R = attn_grid(g, max_items);
-  if (R <= 0) return 0;
-  return attn_items_offset(g.batch, R) + (size_t)4 * max_items;
+  if (attn_grid(g, max_items) <= 0) return 0;
+  return attn_items_offset(g.batch) + (size_t)4 * max_items;
 }
 
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
