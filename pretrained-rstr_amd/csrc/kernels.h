@@ -81,10 +81,13 @@ struct AttnGeom {
 //   lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]   per lane (window
 //       start, first split, split count, and prefixes of its items, full
 //       items and partial items);
+//   ctr arm          the split kernel's claim counter and the value that arms
+//       it (written by the prep, re-armed by the merge after every split);
 //   items[max_items][4] at a 16-byte boundary: the work list, full items then
 //       partial ones, entries (lane | kv head << 20, t0, t1, item index).
 // max_items bounds the step's items (sum over lanes of n_kv * splits).
-inline int lane_tab_words(int batch) { return 6 * batch + 3; }
+__host__ __device__ inline int attn_ctl_offset(int batch) { return 6 * batch + 3; }
+inline int lane_tab_words(int batch) { return 6 * batch + 5; }
 inline size_t attn_items_offset(int batch) { return ((size_t)lane_tab_words(batch) + 3) & ~(size_t)3; }
 int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported geometry
 size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry
@@ -92,7 +95,7 @@ hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* le
                             int32_t* lane_tab, int max_items);
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
-                             const int32_t* page_table, const int32_t* lane_tab, float* part,
+                             const int32_t* page_table, int32_t* lane_tab, float* part,
                              int max_items);
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                              int32_t* lane_tab, const float* part, float* out_f32,

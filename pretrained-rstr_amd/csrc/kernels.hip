@@ -872,7 +872,7 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
 // tokens [max(lo, k*split), min(len, (k+1)*split)).  A split is full when it
 // holds `split` tokens; only a lane's first (window start) and last split can
 // be partial.
-__global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int window, int n_kv,
+__global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int window, int n_kv, int R,
                                                    const int32_t* __restrict__ lengths,
                                                    int32_t* __restrict__ tab) {
   // tab: lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]; base, fbase
@@ -936,6 +936,11 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     base[batch] = carry_a;
     fbase[batch] = carry_f;
     pbase[batch] = carry_p;
+    // the split kernel's R waves take max(0, N/R - 1) static rounds; the
+    // counter hands out the rest of the list
+    const int arm = max(0, carry_a / R - 1) * R;
+    tab[attn_ctl_offset(batch)] = arm;
+    tab[attn_ctl_offset(batch) + 1] = arm;
   }
 }
 
@@ -986,7 +991,7 @@ hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* le
   const int R = attn_grid(g, max_items);
   if (R <= 0) return hipErrorInvalidValue;
   if (g.batch >= (1 << 20) || g.n_kv >= (1 << 11)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv,
+  hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv, R,
                      lengths, lane_tab);
   hipLaunchKernelGGL(k_attn_items, dim3((max_items + 255) / 256), dim3(256), 0, st, g.batch, g.n_kv, g.split,
                      lengths, lane_tab, reinterpret_cast<int4*>(lane_tab + attn_items_offset(g.batch)));
@@ -1028,9 +1033,18 @@ __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlan
 // then k*R + R-1-w, alternating).  The position is wave-uniform, so this is
 // one scalar load.  Prefetched entries stay raw until used, so no wait is
 // placed at the load.
-__device__ __forceinline__ int4 attn_item_raw(const int4* __restrict__ items, int k) {
+// Rounds below ks are static; later ones claim the next unclaimed list
+// position from the launch's counter (armed to ks*R), so waves that run ahead
+// take over the tail.  Entry x < 0: the wave's sequence has ended.
+__device__ __forceinline__ int4 attn_item_fetch(const int4* __restrict__ items, int k, int ks, int n,
+                                                int* __restrict__ ctr) {
   const int R = gridDim.x, w = blockIdx.x;
-  return items[(size_t)k * R + ((k & 1) ? R - 1 - w : w)];
+  if (k < ks) return items[(size_t)k * R + ((k & 1) ? R - 1 - w : w)];
+  int v = 0;
+  if (threadIdx.x == 0) v = atomicAdd(ctr, 1);
+  const int pos = uni(v);
+  if (pos < n) return items[pos];
+  return int4{-1, 0, 0, 0};
 }
 __device__ __forceinline__ AttnItem attn_item_make(int4 d) {
   AttnItem it;
@@ -1049,7 +1063,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
     int n_kv, int page_size, int ps_shift, int pps, float scale,
     const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ n_items,
-    const int4* __restrict__ items, float* __restrict__ part) {
+    const int4* __restrict__ items, int* __restrict__ ctr, float* __restrict__ part) {
   constexpr int NP = HD / 8;             // 16-byte pieces per row
   constexpr int CT = 16;                 // tokens per chunk
   constexpr int CU16 = CT * NP;          // 16-byte units per chunk
@@ -1089,25 +1103,26 @@ __global__ __launch_bounds__(64) void k_attn_split(
     dma_boff[u] = (uint32_t)(dma_r[u] * kvr + dma_off[u]) * 2u;
   }
 
-  // This wave's rounds of the work list: every wave takes N / R full rounds,
-  // and the last round's first N % R positions go to the waves that own them.
-  const int i_begin = 0;
-  int i_end;
-  {
-    const int N = uni(*n_items), R = gridDim.x, w = blockIdx.x;
-    const int kq = N / R, kr = N % R;
-    i_end = kq + ((((kq & 1) ? R - 1 - w : w) < kr) ? 1 : 0);
-  }
-  if (i_end <= 0) return;
+  // This wave's work: ks static rounds of the list (ks = N / R - 1, so the
+  // last one to two rounds of items are claimed dynamically), then claims.
+  const int n_tot = uni(*n_items);
+  const int ks = max(0, n_tot / (int)gridDim.x - 1);
+  int pk = 0;  // rounds fetched
+  const int4 first = attn_item_fetch(items, pk++, ks, n_tot, ctr);
+  if (first.x < 0) return;
 
-  // One continuous stream per wave: the positions of item i are its K
+  // One continuous stream per wave: the positions of an item are its K
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
   // consumer across item boundaries, so the ring never drains between items.
-  int pi = i_begin, ppos = 0;  // producer cursor
-  AttnItem gp = attn_item_make(attn_item_raw(items, pi));
-  int4 gpn = attn_item_raw(items, min(pi + 1, i_end - 1));  // the next item, loaded one item early
-  AttnItem gc = gp;                                          // the consumer's item
-  int4 gcn = gpn;                                            // and its successor
+  // Entries the producer fetched and the consumer has not started wait in a
+  // three-deep FIFO (the producer is at most two items and one prefetch ahead).
+  int ppos = 0;                         // producer position within gp
+  bool pdone = false;                   // producer has issued everything
+  AttnItem gp = attn_item_make(first);  // producer's item
+  int4 gpn = attn_item_fetch(items, pk++, ks, n_tot, ctr);  // the item after gp
+  AttnItem gc = gp;                     // consumer's item
+  int4 fq0 = gpn, fq1 = gpn, fq2 = gpn;
+  int fqn = gpn.x >= 0 ? 1 : 0;
   int pslot = 0;  // ring slot of the producer's next chunk
   // PG16: page_size is a power of two and a multiple of 16, so a chunk lies in
   // one page; pg_next is the page of the producer's next chunk.
@@ -1141,13 +1156,21 @@ __global__ __launch_bounds__(64) void k_attn_split(
     pslot = pslot == RB - 1 ? 0 : pslot + 1;                                                      \
     if (++ppos == 2 * gp.nch) {                                                                   \
       ppos = 0;                                                                                   \
-      if (++pi < i_end) {                                                                         \
+      if (gpn.x >= 0) {                                                                           \
         gp = attn_item_make(gpn);                                                                 \
-        gpn = attn_item_raw(items, min(pi + 1, i_end - 1));                                       \
+        gpn = attn_item_fetch(items, pk++, ks, n_tot, ctr);                                       \
+        if (gpn.x >= 0) {                                                                         \
+          if (fqn == 0) fq0 = gpn;                                                                \
+          else if (fqn == 1) fq1 = gpn;                                                           \
+          else fq2 = gpn;                                                                         \
+          fqn++;                                                                                  \
+        }                                                                                         \
+      } else {                                                                                    \
+        pdone = true;                                                                             \
       }                                                                                           \
     }                                                                                             \
     if constexpr (PG16) {                                                                         \
-      if (pi < i_end) {                                                                           \
+      if (!pdone) {                                                                               \
         const int cn_ = ppos < gp.nch ? ppos : ppos - gp.nch;                                     \
         pg_next = page_table[(size_t)gp.b * pps + ((gp.T0 + cn_ * CT) >> ps_shift)];              \
       }                                                                                           \
@@ -1155,10 +1178,10 @@ __global__ __launch_bounds__(64) void k_attn_split(
   } while (0)
 
   for (int k = 0; k < RB - 1; k++)
-    if (pi < i_end) RSTR_ATTN_ISSUE();
+    if (!pdone) RSTR_ATTN_ISSUE();
 
   // consumer
-  int ci = i_begin, cpos = 0, consumed = 0, cslot = 0;
+  int cpos = 0, consumed = 0, cslot = 0;
   float qv[G][NCL][8];
   // A kv group's G query rows are contiguous: they reach LDS by QB DMA
   // instructions (lanes past the end re-read the last piece).
@@ -1197,7 +1220,7 @@ __global__ __launch_bounds__(64) void k_attn_split(
   }
 
   while (true) {
-    if (pi < i_end) {
+    if (!pdone) {
       // the ring slot being refilled was last read one step ago; its LDS
       // reads (and the prefetched page id) have all returned
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -1290,8 +1313,8 @@ __global__ __launch_bounds__(64) void k_attn_split(
         __asm__ __volatile__("" ::: "memory");
         // the next item's query: its DMA lands while this item's V chunks run
         // (qv itself is reloaded from LDS when the next item starts)
-        if (ci + 1 < i_end) {
-          const AttnItem gn = attn_item_make(gcn);
+        if (fqn > 0) {
+          const AttnItem gn = attn_item_make(fq0);
           RSTR_ATTN_DMA_Q(gn);
           q_dma_step = consumed;
         }
@@ -1377,10 +1400,12 @@ __global__ __launch_bounds__(64) void k_attn_split(
         }
       }
     }
-    if (++ci >= i_end) break;
+    if (fqn == 0) break;
     cpos = 0;
-    gc = attn_item_make(gcn);
-    gcn = attn_item_raw(items, min(ci + 1, i_end - 1));
+    gc = attn_item_make(fq0);
+    fq0 = fq1;
+    fq1 = fq2;
+    fqn--;
     // the query DMA is complete once a position issued after it has been
     // waited for; position p is issued at consumer step p - (RB - 1)
     if (consumed - 1 < q_dma_step + RB) __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -1430,14 +1455,15 @@ struct AttnSplit {
     return std::max(1, std::min(device_cus() * n, max_items));
   }
   static void launch(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
-                     const uint16_t* vp, const int32_t* pt, const int32_t* tab, float* part,
+                     const uint16_t* vp, const int32_t* pt, int32_t* tab, float* part,
                      int max_items) {
     const int R = grid(g, max_items);
     const int32_t* n_items = tab + 4 * g.batch;  // base[batch]
+    int* ctr = tab + attn_ctl_offset(g.batch);
     const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch));
     const int shift = pg16(g) ? __builtin_ctz((unsigned)g.page_size) : 0;
     hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
-                       kp, vp, pt, n_items, items, part);
+                       kp, vp, pt, n_items, items, ctr, part);
   }
 };
 
@@ -1474,7 +1500,7 @@ size_t attn_tab_words(const AttnGeom& g, int max_items) {
 
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
-                             const int32_t* page_table, const int32_t* lane_tab, float* part,
+                             const int32_t* page_table, int32_t* lane_tab, float* part,
                              int max_items) {
 #define RSTR_AL(HD_, G_, L_)                                                                            \
   {                                                                                                     \
@@ -1501,6 +1527,9 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
   const int lane = threadIdx.x;
   const int b = blockIdx.x / n_q, h = blockIdx.x % n_q;
   const int G = n_q / n_kv;
+  // the split kernel of this layer has finished: re-arm its claim counter
+  // for the next split over this table
+  if (blockIdx.x == 0 && lane == 0) tab[attn_ctl_offset(batch)] = tab[attn_ctl_offset(batch) + 1];
   const int ns = tab[2 * batch + b];
   const int base = tab[3 * batch + b] + (h / G) * ns;
   const int hl = h % G;
