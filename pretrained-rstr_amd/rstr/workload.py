@@ -19,6 +19,7 @@ import time
 
 import numpy as np
 
+from . import residency
 from .page_pool import PagePool, PagePoolError
 from .paged_decoder import PagedDecoder
 
@@ -62,7 +63,7 @@ class ChurnPlanner:
 
     def __init__(self, cfg: dict, batch: int, page_size: int, physical_pages: int, maxpos: int,
                  seed: int, arrival_mean: float = 4.0, prompt=(128, 4096), output=(32, 512),
-                 fill_seed: int = 7, warm_start: bool = True):
+                 fill_seed: int = 7, warm_start: bool = True, retain_finished: bool = False):
         self.cfg, self.batch, self.maxpos = cfg, batch, maxpos
         self.rng = np.random.default_rng(seed)
         self.arrival_mean, self.prompt, self.output = arrival_mean, prompt, output
@@ -79,6 +80,11 @@ class ChurnPlanner:
         self.host_seconds = 0.0
         self.retired = 0
         self.rejected_admissions = 0
+        # retain_finished: finished continuations stay resident as durable
+        # routes (a prefix cache) and admissions evict them by value
+        # (residency.clj) when the pool runs short
+        self.retain_finished = retain_finished
+        self.evicted = 0
 
     def _arrive(self, n):
         for _ in range(n):
@@ -90,11 +96,20 @@ class ChurnPlanner:
 
     def _admit(self, lane, req, progress=0):
         cid = req["id"]
-        try:
-            cap = self.pool.reserve_capacity(cid, req["prompt"] + req["output"])
-        except PagePoolError:
-            self.rejected_admissions += 1
-            return False
+        if self.retain_finished:
+            plan = residency.reserve_admission(self.pool, cid, req["prompt"] + req["output"],
+                                               {st["cid"] for st in self.lanes if st is not None})
+            if not plan["admissible?"]:
+                self.rejected_admissions += 1
+                return False
+            self.evicted += len(plan["evictions"])
+            cap = plan["capacity-reservation"]
+        else:
+            try:
+                cap = self.pool.reserve_capacity(cid, req["prompt"] + req["output"])
+            except PagePoolError:
+                self.rejected_admissions += 1
+                return False
         route = self.pool.allocate_route(cid, req["prompt"] - 1 + progress, capacity_reservation=cap)
         self.rec.fill(route.pages)
         self.dec.prime_lanes([{"lane": lane, "token": req["token"]}])
@@ -128,7 +143,14 @@ class ChurnPlanner:
                 continue
             st["left"] -= 1
             if st["left"] <= 0:
-                self.pool.release_route(st["cid"])
+                if self.retain_finished:
+                    r = self.pool.route(st["cid"])
+                    self.pool.touch_route(st["cid"], {
+                        "durable?": True, "last-access": self.steps_planned,
+                        "reuse-probability": float(self.rng.uniform(0.0, 1.0)),
+                        "recompute-ms": 0.05 * r.token_count, "reload-ms": 0.01 * r.token_count})
+                else:
+                    self.pool.release_route(st["cid"])
                 self.pool.release_capacity(st["cap"])
                 self.lanes[lane] = None
                 self.retired += 1
