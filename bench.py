@@ -36,6 +36,117 @@ WORKLOADS = {
 }
 
 
+# isolated attention workloads: (model shape, lanes, seed)
+ATTN_WORKLOADS = {"config4": ("llama3_8b", 128, 4)}
+
+
+def attention_workload(args) -> dict:
+    """Config 4: one layer's routed paged attention alone.  128 lanes of a
+    Llama-3-8B-shaped layer (32/8 heads, hd 128), contexts lognormal(7, 1.2)
+    clipped to [16, 32768] (seed 4), page ids permuted, and the first quarter of
+    every lane's full pages drawn from one shared run of pages (a common prefix),
+    so 25% of full pages are shared across lanes.  Reports logical and unique KV
+    GB/s of the split kernel (merge timed beside it)."""
+    name, B, seed = ATTN_WORKLOADS[args.workload]
+    cfg = dict(configs.MODELS[name], n_layers=1)
+    ps, n_kv, hd, n_q = 16, cfg["n_kv"], cfg["head_dim"], cfg["n_q"]
+    rng = np.random.default_rng(seed)
+    lengths = np.clip(np.rint(np.exp(rng.normal(7.0, 1.2, B))), 16, 32768).astype(np.int32)
+    full = lengths // ps
+    npages = -(-lengths // ps)
+    shared_n = np.rint(0.25 * full).astype(np.int64)
+    S = int(shared_n.max())
+    private = int((npages - shared_n).sum())
+    physical = S + private
+    perm = rng.permutation(physical).astype(np.int32)
+    shared_pages, priv_pages = perm[:S], perm[S:]
+    pps = int(npages.max())
+    pt = np.full((B, pps), -1, np.int32)
+    used = 0
+    for b in range(B):
+        k = int(shared_n[b])
+        pt[b, :k] = shared_pages[:k]
+        n_priv = int(npages[b]) - k
+        pt[b, k:npages[b]] = priv_pages[used:used + n_priv]
+        used += n_priv
+    row_bytes = n_kv * hd * 2 * 2  # fp16 K + V of one token
+    logical = int(lengths.sum()) * row_bytes
+    unique_tokens = int(shared_n.max()) * ps + int((lengths - shared_n * ps).sum())
+    unique = unique_tokens * row_bytes
+    sess = hip.Session(0)
+    model = hip.Model(sess, cfg, seed=1)
+    pool = hip.Pool(model, ps, physical)
+    pool.fill_synthetic(np.arange(physical, dtype=np.int32), seed)
+    q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+    pool.attention_bench(0, q, pt, lengths, split=args.split, iters=max(1, args.warmup))
+    split_ms, merge_ms = pool.attention_bench(0, q, pt, lengths, split=args.split, iters=args.steps)
+    log(f"config4: {B} lanes, mean ctx {lengths.mean():.0f}, max {lengths.max()}, {physical} pages; "
+        f"logical {logical / 1e9:.3f} GB, unique {unique / 1e9:.3f} GB per launch; "
+        f"split {split_ms * 1e3:.1f} us, merge {merge_ms * 1e3:.1f} us")
+    gbs = logical / (split_ms * 1e-3) / 1e9
+    ugbs = unique / (split_ms * 1e-3) / 1e9
+    out = {
+        "metric": "paged attention KV GB/s (logical bytes per split launch); % of HBM roofline on 1 MI355X",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(split_ms + merge_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 KV, fp32 accumulate",
+        "data": "synthetic (seeded fp16 page templates, N(0,1) queries)",
+        "config": {"workload": f"config4: isolated paged attention, {B} lanes, {n_q}/{n_kv} heads, hd {hd}, "
+                               "ctx lognormal(7,1.2) clipped [16,32768], 25% of full pages shared",
+                   "lanes": B, "page_size": ps, "physical_pages": physical, "attention_split": args.split,
+                   "mean_ctx": round(float(lengths.mean()), 1), "parallelism": "1 GPU (replica)"},
+        "roofline": {"bound": "hbm", "achieved": round(ugbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ugbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_attn_split (unique KV bytes per launch)", "bytes_per_launch": unique,
+                     "avg_launch_ms": round(split_ms, 4)},
+        "logical_bytes_per_launch": logical, "merge_ms": round(merge_ms, 4),
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_attention_baseline(q, lengths, ps, n_kv, hd, cfg["attn_scale"], args.split,
+                                                         args.cpu_seconds)
+        except Exception as e:  # the baseline must not hide the GPU number
+            out["cpu_baseline"] = {"error": repr(e)}
+    pool.close()
+    model.close()
+    sess.close()
+    return out
+
+
+def cpu_attention_baseline(q, lengths, ps, n_kv, hd, scale, split, budget_s) -> dict:
+    """The oracle's routed attention (paged_attention.clj:196-228 restated in C,
+    OpenMP over lanes) on host fp16 pages: lanes of the same workload taken in
+    order until the sample holds about 1/16 of the logical bytes, repeated for
+    about ``budget_s`` seconds."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker / CPU baseline only
+    total = int(lengths.sum())
+    n = 1
+    while n < len(lengths) and int(lengths[:n].sum()) < total // 16:
+        n += 1
+    sub = lengths[:n]
+    npg = -(-sub // ps)
+    pt = np.full((n, int(npg.max())), -1, np.int32)
+    off = 0
+    for b in range(n):
+        pt[b, :npg[b]] = np.arange(off, off + npg[b])
+        off += int(npg[b])
+    rng = np.random.default_rng(4)
+    kp = rng.standard_normal((off, ps, n_kv, hd)).astype(np.float16)
+    vp = rng.standard_normal((off, ps, n_kv, hd)).astype(np.float16)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.attention(q[:n], kp, vp, pt, sub, 0, scale, split)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    nbytes = int(sub.sum()) * n_kv * hd * 2 * 2
+    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": int(O.lib().orc_num_threads()),
+            "kind": "port",
+            "sample": f"{n} of {len(lengths)} lanes ({int(sub.sum())} of {total} tokens), {reps} launches"}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -79,7 +190,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--pool-fraction", type=float, default=0.8)
     ap.add_argument("--split", type=int, default=256)
@@ -92,6 +203,9 @@ def main():
                                    "page pools, so one GPU's throughput is the per-replica figure)"}))
         sys.exit(2)
 
+    if args.workload in ATTN_WORKLOADS:
+        print(json.dumps(attention_workload(args)), flush=True)
+        return
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
     cfg = configs.MODELS[name]
     pps = -(-maxpos // ps)

@@ -248,6 +248,47 @@ def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
         m.close()
 
 
+def test_attention_long_shared_routes_match_oracle(sess):
+    """Config-4 geometry (32/8 heads, hd 128): long routes (many splits), pages
+    shared across lanes (a common prefix run), permuted page ids."""
+    print("case attention long shared routes", flush=True)
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=32, n_kv=8, head_dim=128)
+    ps = 16
+    lengths = np.array([16, 300, 5000, 4097, 33, 8000, 0, 2049], np.int32)
+    B = len(lengths)
+    rng = np.random.default_rng(44)
+    shared = 40  # the first min(40, full pages) pages of every lane are one shared run
+    npg = -(-lengths // ps)
+    priv = int(np.maximum(npg - np.minimum(lengths // ps, shared), 0).sum())
+    pages = shared + priv
+    perm = rng.permutation(pages).astype(np.int32)
+    pps = int(npg.max())
+    pt = np.full((B, pps), -1, np.int32)
+    used = shared
+    for b in range(B):
+        k = int(min(lengths[b] // ps, shared))
+        pt[b, :k] = perm[:k]
+        n = int(npg[b]) - k
+        pt[b, k:npg[b]] = perm[used:used + n]
+        used += n
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, 8, 128)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, 8, 128)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        q = rng.standard_normal((B, 32, 128)).astype(np.float32)
+        scale = 1.0 / math.sqrt(128)
+        got = p.attention(0, q, pt, lengths, scale=scale, split=256)
+        want = O.attention(q, kp, vp, pt, lengths, 0, scale, 256)
+        assert np.array_equal(got, want)
+        assert np.all(got[6] == 0)
+    finally:
+        p.close()
+        m.close()
+
+
 # ---------------------------------------------------------------------------
 # full decode steps
 # ---------------------------------------------------------------------------
