@@ -33,6 +33,9 @@ WORKLOADS = {
     # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
     "config5": ("llama3_8b", 128, 16, 4096 + 512, (128, 4096), (32, 512), 4.0, 5),
     "config2": ("gemma3_270m", 16, 16, 2048 + 256 + 1, (64, 2048), (256, 256), 0.0, 1),
+    # config 3: contexts log-uniform [256, 8192], lanes 0-31 fork one 1024-token prefix
+    # (prompt/output None selects the shared-prefix planner)
+    "config3": ("qwen3_06b", 64, 16, 8192 + 512, None, None, 0.0, 2),
 }
 
 
@@ -225,8 +228,11 @@ def main():
 
     # ---- plan the whole run on the host (control-plane mirror) -------------------------
     n_total = args.warmup + args.steps + args.profile_steps
-    planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed, arrival_mean=arrivals,
-                                    prompt=prompt, output=output)
+    if prompt is None:
+        planner = workload.SharedPrefixPlanner(cfg, lanes, ps, physical, maxpos, seed=seed)
+    else:
+        planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed, arrival_mean=arrivals,
+                                        prompt=prompt, output=output)
     t0 = time.perf_counter()
     plan = [planner.plan_step() for _ in range(n_total)]
     plan_s = time.perf_counter() - t0
@@ -246,7 +252,10 @@ def main():
     ms_per_step = dev_ms / args.steps
     value = tokens / (dev_ms / 1e3)
     bytes_steps = [workload.step_bytes(cfg, st, model.weight_bytes) for st in timed]
-    step_bytes = float(np.mean([b["total"] for b in bytes_steps]))
+    # unique physical KV rows (pages shared by lanes count once) where the step has a
+    # page table without windows; logical rows otherwise
+    step_bytes = float(np.mean([b.get("total_unique", b["total"]) for b in bytes_steps]))
+    step_bytes_logical = float(np.mean([b["total"] for b in bytes_steps]))
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"timed {args.steps} steps: {dev_ms:.1f} ms, {ms_per_step:.3f} ms/step, {value:.0f} tok/s, "
         f"{step_bytes / 1e9:.2f} GB/step algorithmic -> {step_gbs:.0f} GB/s")
@@ -255,8 +264,11 @@ def main():
     first = args.warmup + args.steps
     prof = dec.profile_steps(first, args.profile_steps)
     prof_plan = plan[first:first + args.profile_steps]
-    attn_bytes = np.mean([np.mean(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in prof_plan])
-    all_bytes = np.mean([np.mean(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in plan])
+    def layer_kv(st):
+        b = workload.step_bytes(cfg, st, 0)
+        return b.get("kv_unique_per_layer", np.mean(b["kv_per_layer"]))
+    attn_bytes = np.mean([layer_kv(st) for st in prof_plan])
+    all_bytes = np.mean([layer_kv(st) for st in plan])
     log(f"attention algorithmic bytes per launch: {all_bytes:.0f} (all {len(plan)} steps), "
         f"{attn_bytes:.0f} (profiled steps)")
     attn_ms, attn_n = prof["attn_split"]
@@ -275,24 +287,29 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4/int8 block dots exact, fp32 accumulate, fp16 KV",
-        "data": "synthetic (seeded random-init weights, synthetic prefix K/V, Poisson churn)",
-        "config": {"workload": f"{args.workload}: {name}-shaped Q4 decoder, {lanes} continuous lanes, "
-                               f"prompts U{list(prompt)}, outputs U{list(output)}, "
-                               f"Poisson({arrivals}) arrivals/step",
+        "data": "synthetic (seeded random-init weights, synthetic prefix K/V, "
+                + ("Poisson churn)" if prompt is not None else "shared-prefix forks)"),
+        "config": {"workload": (f"{args.workload}: {name}-shaped Q4 decoder, {lanes} continuous lanes, "
+                                f"prompts U{list(prompt)}, outputs U{list(output)}, "
+                                f"Poisson({arrivals}) arrivals/step") if prompt is not None else
+                               (f"{args.workload}: {name}-shaped Q4 decoder, {lanes} decode lanes, contexts "
+                                f"log-uniform[256, 8192], lanes 0-31 fork one 1024-token prefix "
+                                f"(copy-on-write on the first divergent append); {planner.cow_pages} pages copied"),
                    "lanes": lanes, "page_size": ps, "physical_pages": physical,
                    "attention_split": args.split, "parallelism": "1 GPU (replica)"},
         "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_attn_split (paged attention, per layer launch)",
                      "bytes_per_launch": int(attn_bytes), "avg_launch_ms": round(attn_avg_ms, 4)},
-        "step_roofline": {"bytes_per_step": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
-                          "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "step_roofline": {"bytes_per_step": int(step_bytes), "logical_bytes_per_step": int(step_bytes_logical),
+                          "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "kernel_ms_per_step": {k: round(v[0] / args.profile_steps, 3) for k, v in prof.items()},
         "host_bookkeeping_ms_per_step": round(host_ms_step, 3),
     }
     if not args.no_cpu_baseline:
         try:
-            out["cpu_baseline"] = cpu_baseline(cfg, prefix=int(np.mean(prompt)), budget_s=args.cpu_seconds)
+            mean_ctx = int(np.mean(prompt)) if prompt is not None else int(np.mean(plan[0]["lengths"]))
+            out["cpu_baseline"] = cpu_baseline(cfg, prefix=mean_ctx, budget_s=args.cpu_seconds)
         except Exception as e:  # the baseline must not hide the GPU number
             out["cpu_baseline"] = {"error": repr(e)}
     dec.close()

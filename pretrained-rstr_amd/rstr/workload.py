@@ -162,6 +162,73 @@ class ChurnPlanner:
         return out
 
 
+class SharedPrefixPlanner:
+    """A fixed set of decode lanes whose first ``shared_lanes`` fork one resident
+    prefix: contexts log-uniform in ``ctx``; a lane of
+    the shared group forks the prefix route at min(ctx, prefix) - 1 rows
+    (``fork-route!``, page_pool.clj:679-724) and appends its private rows with a
+    range reservation, so the shared partial tail page is copied on the first
+    divergent append (page_pool.clj:923-944); the other lanes hold private
+    routes.  Every lane then decodes every step (no retirement)."""
+
+    def __init__(self, cfg: dict, batch: int, page_size: int, physical_pages: int, maxpos: int,
+                 seed: int, ctx=(256, 8192), shared_lanes: int = 32, prefix: int = 1024, fill_seed: int = 7):
+        self.cfg, self.batch, self.maxpos = cfg, batch, maxpos
+        self.rng = np.random.default_rng(seed)
+        self.ctx, self.shared_lanes, self.prefix = ctx, shared_lanes, prefix
+        self.fill_seed = fill_seed
+        self.rec = RecordingDevice()
+        self.pool = PagePool(page_size, physical_pages, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"],
+                             device=self.rec)
+        self.dec = PagedDecoder(self.pool, self.rec, batch_size=batch, maxpos=maxpos)
+        self.steps_planned = 0
+        self.host_seconds = 0.0
+        self.retired = 0
+        self.rejected_admissions = 0
+        self.cow_pages = 0
+
+    def _start(self):
+        lo, hi = np.log(self.ctx[0]), np.log(self.ctx[1])
+        ctx = np.exp(self.rng.uniform(lo, hi, self.batch)).astype(np.int64)
+        root = "prefix"
+        r = self.pool.allocate_route(root, self.prefix - 1)
+        self.rec.fill(r.pages)
+        for lane in range(self.batch):
+            c = int(ctx[lane])
+            if lane < self.shared_lanes:
+                n = min(c, self.prefix) - 1
+                self.pool.fork_route(root, lane, n)
+                extra = c - 1 - n
+                if extra > 0:
+                    res = self.pool.reserve_append_range(lane, extra)
+                    self.rec.fill(res.added_pages)
+                    self.pool.commit_append(lane, res)
+            else:
+                self.rec.fill(self.pool.allocate_route(lane, c - 1).pages)
+            tok = int(self.rng.integers(0, self.cfg["vocab"]))
+            self.dec.prime_lanes([{"lane": lane, "token": tok}])
+        # the lanes hold their own references; the prefix stays resident for reuse
+        self.pool.touch_route(root, {"durable?": True})
+
+    def plan_step(self) -> dict:
+        t0 = time.perf_counter()
+        self.rec.begin()
+        if self.steps_planned == 0:
+            self._start()
+        work = []
+        for lane in range(self.batch):
+            r = self.pool.route(lane)
+            work.append({"lane": lane, "continuation_id": lane, "position": r.start_position + r.token_count})
+        self.dec.step_lanes(work)
+        out = self.rec.end()
+        self.cow_pages += len(out["cow_pairs"])
+        out["fill_seed"] = self.fill_seed
+        out["active"] = len(work)
+        self.steps_planned += 1
+        self.host_seconds += time.perf_counter() - t0
+        return out
+
+
 def step_bytes(cfg: dict, step: dict, weight_bytes: int) -> dict:
     """Algorithmic HBM bytes of one decode step: packed weights once, the visible
     fp16 K+V of every layer (window-limited on local layers; logical rows, which
@@ -178,5 +245,24 @@ def step_bytes(cfg: dict, step: dict, weight_bytes: int) -> dict:
     kv = sum(per_layer_kv)
     appends = int(active.sum()) * L * kvr * 2 * 2
     gather = int(active.sum()) * d * 4
-    return {"weights": weight_bytes, "kv": kv, "kv_per_layer": per_layer_kv, "appends": appends,
-            "gather": gather, "total": weight_bytes + kv + appends + gather}
+    out = {"weights": weight_bytes, "kv": kv, "kv_per_layer": per_layer_kv, "appends": appends,
+           "gather": gather, "total": weight_bytes + kv + appends + gather}
+    if "page_table" in step and cfg["sliding_window"] <= 0:
+        # physical pages shared by several lanes count once (the rows any lane reads)
+        ps = int(step.get("page_size", 16))
+        pt = np.asarray(step["page_table"], np.int64).reshape(len(lengths), -1)
+        lanes = np.nonzero(active)[0]
+        n = lengths[lanes]
+        npg = -(-n // ps)
+        lane_of = np.repeat(lanes, npg)
+        idx = np.arange(int(npg.sum())) - np.repeat(np.cumsum(npg) - npg, npg)
+        pg = pt[lane_of, idx]
+        rows = np.minimum(ps, np.repeat(n, npg) - idx * ps)
+        order = np.argsort(pg, kind="stable")
+        pg, rows = pg[order], rows[order]
+        starts = np.concatenate([[0], np.flatnonzero(np.diff(pg)) + 1]) if pg.size else np.zeros(0, np.int64)
+        ukv = int(np.maximum.reduceat(rows, starts).sum()) * kvr * 2 * 2 if pg.size else 0
+        out["kv_unique_per_layer"] = ukv
+        out["kv_unique"] = ukv * L
+        out["total_unique"] = weight_bytes + ukv * L + appends + gather
+    return out
