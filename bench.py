@@ -29,6 +29,10 @@ from rstr import configs, hip, workload  # noqa: E402
 METRIC = "aggregate decode tokens/sec at N lanes; % of HBM roofline (GB/s) on 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 
+# attention split per workload (the split fixes the canonical reduction order, so it is a
+# decoder parameter): the largest that still gives every resident wave several items
+SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256}
+
 WORKLOADS = {
     # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
     "config5": ("llama3_8b", 128, 16, 4096 + 512, (128, 4096), (32, 512), 4.0, 5),
@@ -196,10 +200,12 @@ def main():
     ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--pool-fraction", type=float, default=0.8)
-    ap.add_argument("--split", type=int, default=256)
+    ap.add_argument("--split", type=int, default=None, help="attention split (default: per workload)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
+    if args.split is None:
+        args.split = SPLITS[args.workload]
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (the decode step "
                                    "shards as independent per-GPU replicas with their own lanes and "
