@@ -1,0 +1,74 @@
+"""The bench's timed path: host-planned step schedules uploaded once
+(``rstr_schedule_upload``) and replayed on the device (``rstr_schedule_run``:
+synthetic prefix fills, copy-on-write page copies, lane primes, one step graph
+per step) against the oracle replaying the same recorded steps in the same
+order, token for token.  Covers continuous churn (with value-based retention of
+finished routes) and forked shared prefixes with copy-on-write."""
+import numpy as np
+import pytest
+
+import oracle as O
+from rstr import configs, hip, workload
+
+CFG = configs.MODELS["tiny_llama"]
+
+
+def _replay_oracle(od, steps):
+    out = []
+    for st in steps:
+        for pg in st["fill_pages"]:
+            od.fill_synthetic(int(pg), int(st["fill_seed"]))
+        for src, dst in st["cow_pairs"]:
+            od.copy_page(int(src), int(dst))
+        if st["prime_lanes"]:
+            od.prime_lanes(st["prime_lanes"], st["prime_tokens"])
+        out.append(od.step_lanes(st["slots"], st["row_offsets"], st["positions"], st["page_table"],
+                                 st["lengths"], st["start_positions"]))
+    return np.array(out)
+
+
+def _check(planner_factory, batch, pages, maxpos, split, n_steps):
+    pps = -(-maxpos // 16)
+    pl = planner_factory(pages, pps)
+    steps = [pl.plan_step() for _ in range(n_steps)]
+    om = O.Model(CFG, seed=3)
+    od = O.Decoder(om, batch, 16, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        want = _replay_oracle(od, steps)
+    finally:
+        od.close()
+        om.close()
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=3)
+        p = hip.Pool(m, 16, pages)
+        d = hip.Decoder(m, p, batch, pps, maxpos, split)
+        d.schedule_upload(steps)
+        got, _ = d.schedule_run(0, n_steps)
+    for i, st in enumerate(steps):
+        act = np.asarray(st["lengths"]) > 0
+        assert np.array_equal(got[i][act], want[i][act]), (i, got[i], want[i])
+    return pl
+
+
+@pytest.mark.gpu
+def test_schedule_replay_with_churn_matches_oracle():
+    print("case schedule churn", flush=True)
+    batch, pages, maxpos = 6, 60, 192
+
+    def make(pages, pps):
+        return workload.ChurnPlanner(CFG, batch, 16, pages, maxpos, seed=11, arrival_mean=1.5,
+                                     prompt=(8, 60), output=(2, 12), retain_finished=True)
+    pl = _check(make, batch, pages, maxpos, 16, 40)
+    assert pl.retired > 0 and pl.evicted > 0
+
+
+@pytest.mark.gpu
+def test_schedule_replay_with_shared_prefix_forks_matches_oracle():
+    print("case schedule shared prefix", flush=True)
+    batch, pages, maxpos = 6, 200, 400
+
+    def make(pages, pps):
+        return workload.SharedPrefixPlanner(CFG, batch, 16, pages, maxpos, seed=2, ctx=(20, 200),
+                                            shared_lanes=3, prefix=64)
+    pl = _check(make, batch, pages, maxpos, 32, 12)
+    assert pl.cow_pages > 0
