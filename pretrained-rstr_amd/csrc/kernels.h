@@ -83,11 +83,16 @@ struct AttnGeom {
 //       items and partial items);
 //   ctr arm          the split kernel's claim counter and the value that arms
 //       it (written by the prep, re-armed by the merge after every split);
+//   boff[RSTR_NCH] cur[RSTR_NCH]   partial items by chunk count: list offset
+//       of each count (larger counts first) and the fill cursor of each;
 //   items[max_items][4] at a 16-byte boundary: the work list, full items then
-//       partial ones, entries (lane | kv head << 20, t0, t1, item index).
+//       partial ones by decreasing chunk count, entries
+//       (lane | kv head << 20, t0, t1, item index).
 // max_items bounds the step's items (sum over lanes of n_kv * splits).
+#define RSTR_NCH 260  // chunk counts of one split (split <= 4096 tokens)
 __host__ __device__ inline int attn_ctl_offset(int batch) { return 6 * batch + 3; }
-inline int lane_tab_words(int batch) { return 6 * batch + 5; }
+__host__ __device__ inline int attn_bucket_offset(int batch) { return 6 * batch + 5; }
+inline int lane_tab_words(int batch) { return 6 * batch + 5 + 2 * RSTR_NCH; }
 inline size_t attn_items_offset(int batch) { return ((size_t)lane_tab_words(batch) + 3) & ~(size_t)3; }
 int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported geometry
 size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry

@@ -878,7 +878,7 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
   // tab: lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]; base, fbase
   // and pbase are exclusive prefix sums over lanes of the lane's items, full
   // items and partial items (integer sums: any order is exact)
-  __shared__ int32_t s_a[1024], s_f[1024], s_p[1024];
+  __shared__ int32_t s_a[1024], s_f[1024], s_p[1024], s_h[RSTR_NCH];
   int32_t* lo = tab;
   int32_t* k0 = tab + batch;
   int32_t* ns = tab + 2 * batch;
@@ -887,6 +887,8 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
   int32_t* pbase = tab + 5 * batch + 2;
   const int tid = threadIdx.x;
   int32_t carry_a = 0, carry_f = 0, carry_p = 0;
+  for (int i = tid; i < RSTR_NCH; i += 1024) s_h[i] = 0;
+  __syncthreads();
   for (int b0 = 0; b0 < batch; b0 += 1024) {
     const int b = b0 + tid;
     int l0 = 0, kk0 = 0, n = 0, f = 0;
@@ -896,9 +898,16 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
         l0 = window > 0 ? max(0, len - window) : 0;
         kk0 = l0 / split;
         n = (len - 1) / split - kk0 + 1;
-        const bool first_full = l0 == kk0 * split && min(len, (kk0 + 1) * split) - l0 == split;
+        const int f_t1 = min(len, (kk0 + 1) * split);
+        const bool first_full = l0 == kk0 * split && f_t1 - l0 == split;
         const bool last_full = len % split == 0;
         f = n == 1 ? (first_full ? 1 : 0) : n - (first_full ? 0 : 1) - (last_full ? 0 : 1);
+        // partial splits by chunk count (n_kv items each)
+        if (!first_full) atomicAdd(&s_h[(f_t1 - (l0 & ~15) + 15) >> 4], n_kv);
+        if (n > 1 && !last_full) {
+          const int lt0 = (kk0 + n - 1) * split;
+          atomicAdd(&s_h[(len - (lt0 & ~15) + 15) >> 4], n_kv);
+        }
       }
       lo[b] = l0;
       k0[b] = kk0;
@@ -941,6 +950,14 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     const int arm = max(0, carry_a / R - 1) * R;
     tab[attn_ctl_offset(batch)] = arm;
     tab[attn_ctl_offset(batch) + 1] = arm;
+    // list offsets of the partial items by decreasing chunk count
+    int32_t acc = 0;
+    int32_t* boff = tab + attn_bucket_offset(batch);
+    for (int c = RSTR_NCH - 1; c >= 0; c--) {
+      boff[c] = acc;
+      boff[RSTR_NCH + c] = 0;  // fill cursor
+      acc += s_h[c];
+    }
   }
 }
 
@@ -952,7 +969,7 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
 // Built once per step, read by every layer.
 __global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int split,
                                                     const int32_t* __restrict__ lengths,
-                                                    const int32_t* __restrict__ tab,
+                                                    int32_t* __restrict__ tab,
                                                     int4* __restrict__ items) {
   const int32_t* lo_t = tab;
   const int32_t* k0_t = tab + batch;
@@ -981,8 +998,15 @@ __global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int spl
   const bool first_partial = !(l0 == k0_t[b] * split && min(len, (k0_t[b] + 1) * split) - l0 == split);
   const int before = (first_partial && s > 0) ? 1 : 0;  // partial splits ahead of s
   int pos;
-  if (t1 - t0 == split) pos = fbase[b] + kvh * nf + (s - before);
-  else pos = fbase[batch] + pbase[b] + kvh * (ns - nf) + before;
+  if (t1 - t0 == split) {
+    pos = fbase[b] + kvh * nf + (s - before);
+  } else {
+    // partial items follow the full ones, larger chunk counts first (the
+    // order inside one count is immaterial)
+    const int nch = (t1 - (t0 & ~15) + 15) >> 4;
+    int32_t* boff = tab + attn_bucket_offset(batch);
+    pos = fbase[batch] + boff[nch] + atomicAdd(boff + RSTR_NCH + nch, 1);
+  }
   items[pos] = int4{b | (kvh << 20), t0, t1, i};
 }
 
