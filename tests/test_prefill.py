@@ -1,0 +1,136 @@
+"""Bulk paged prefill tiles (``PagedDecoder.prefill_range``, paged_decoder.clj:638-711):
+a prompt's uncached suffix goes through the layers ``prefill_T`` rows at a time
+(rows as lanes of a prefill decoder with causal lengths, one M = T projection
+tile per linear), then decoding continues.  The result must equal token-by-token
+priming bit for bit: the same K/V in every page of every layer and the same
+generated tokens.
+
+- CPU: the oracle decoder with prefill tiles vs the oracle decoding token by token.
+- GPU: the HIP decoders (a 1-lane decode decoder and a T-lane prefill decoder on
+  one pool) vs the oracle decoding token by token.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from rstr import configs, hip
+from rstr.page_pool import PagePool
+from rstr.paged_decoder import PagedDecoder, HipStepDevice, prefill_lane_descriptors, DESCRIPTOR_KEYS
+
+CFG = configs.MODELS["tiny_llama"]
+PS, PAGES, MAXPOS, SPLIT, SEED, T = 16, 40, 160, 32, 9, 24
+PPS = MAXPOS // PS
+PROMPT = [int(x) for x in np.random.default_rng(3).integers(0, CFG["vocab"], 61)]
+MAX_NEW = 5
+
+
+def _pad_lanes(desc, batch):
+    """A one-lane decode step as a ``batch``-lane step whose other lanes are idle."""
+    pt = np.asarray(desc["page_table"], np.int32).ravel()
+    out = {"slots": np.full(batch, -1, np.int32), "row_offsets": np.arange(batch + 1, dtype=np.int32),
+           "positions": np.zeros(batch, np.int32), "page_table": np.full((batch, pt.size), -1, np.int32),
+           "lengths": np.zeros(batch, np.int32), "start_positions": np.zeros(batch, np.int32)}
+    out["slots"][0] = np.asarray(desc["slots"]).ravel()[0]
+    out["positions"][0] = np.asarray(desc["positions"]).ravel()[0]
+    out["page_table"][0] = pt
+    out["lengths"][0] = np.asarray(desc["lengths"]).ravel()[0]
+    out["start_positions"][0] = np.asarray(desc["start_positions"]).ravel()[0]
+    out["page_table"] = out["page_table"].ravel()
+    return out
+
+
+class OracleDevice:
+    """Step and prefill protocol over one oracle decoder: lane 0 decodes (the
+    other lanes idle), a prefill tile uses lanes 0..T-1, and the prompt's last
+    token is primed into lane 0 afterwards."""
+
+    def __init__(self, od):
+        self.od, self._d, self._p, self._tok, self.tiles = od, None, None, None, 0
+
+    def upload(self, desc):
+        self._d = _pad_lanes(desc, self.od.batch)
+
+    def run(self):
+        self._tok = self.od.step_lanes(**self._d)[:1]
+
+    def download_tokens(self):
+        return self._tok
+
+    def prime_rows(self, lane_tokens):
+        if lane_tokens:
+            self.od.prime_lanes([lt["lane"] for lt in lane_tokens], [lt["token"] for lt in lane_tokens])
+
+    def copy_page(self, src, dst):
+        self.od.copy_page(src, dst)
+
+    def upload_prefill(self, desc):
+        self._p = prefill_lane_descriptors(desc, self.od.batch)
+
+    def run_prefill(self):
+        self.od.prime_lanes(self._p["lanes"], self._p["tokens"])
+        self.od.step_lanes(**{k: self._p[k] for k in DESCRIPTOR_KEYS})
+        self.tiles += 1
+
+
+def _generate(device, batch_of_pool_device, prefill_T):
+    pool = PagePool(PS, PAGES, CFG["n_layers"], CFG["n_kv"], CFG["head_dim"], device=batch_of_pool_device)
+    dec = PagedDecoder(pool, device, batch_size=1, maxpos=MAXPOS, pages_per_sequence=PPS, prefill_T=prefill_T)
+    toks = dec.generate("c", PROMPT, MAX_NEW)
+    return toks, pool.route("c").pages
+
+
+def _oracle_token_by_token():
+    om = O.Model(CFG, seed=SEED)
+    od = O.Decoder(om, 1, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=SPLIT)
+    try:
+        toks, pages = _generate(OracleDevice(od), od, None)
+        slabs = [(od.slab(s, l).view(np.uint16).copy()) for l in range(CFG["n_layers"]) for s in (0, 1)]
+        return toks, pages, slabs
+    finally:
+        od.close()
+        om.close()
+
+
+def test_prefill_lane_descriptors_are_causal_rows_of_one_route():
+    desc = {"tokens": [5, 6, 7], "slots": [33, 34, 35], "row_offsets": [0, 3], "positions": [17, 18, 19],
+            "page_table": [4, 2, -1], "lengths": [20], "start_positions": [0]}
+    d = prefill_lane_descriptors(desc, 4)
+    assert d["lengths"].tolist() == [18, 19, 20, 0]
+    assert d["slots"].tolist() == [33, 34, 35, -1]
+    assert d["page_table"].reshape(4, 3).tolist() == [[4, 2, -1]] * 3 + [[-1, -1, -1]]
+    assert d["row_offsets"].tolist() == [0, 1, 2, 3, 4]
+
+
+def test_oracle_prefill_tiles_equal_token_by_token_priming():
+    want_toks, want_pages, want_slabs = _oracle_token_by_token()
+    om = O.Model(CFG, seed=SEED)
+    od = O.Decoder(om, T, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=SPLIT)
+    try:
+        dev = OracleDevice(od)
+        toks, pages = _generate(dev, od, T)
+        assert dev.tiles == (len(PROMPT) - 1) // T == 2
+        assert toks == want_toks
+        assert pages == want_pages
+        for i, (l, s) in enumerate((l, s) for l in range(CFG["n_layers"]) for s in (0, 1)):
+            assert np.array_equal(od.slab(s, l).view(np.uint16), want_slabs[i]), (l, s)
+    finally:
+        od.close()
+        om.close()
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_tiles_equal_oracle_token_by_token():
+    print("case prefill tiles", flush=True)
+    want_toks, want_pages, want_slabs = _oracle_token_by_token()
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=SEED)
+        p = hip.Pool(m, PS, PAGES)
+        d1 = hip.Decoder(m, p, 1, PPS, MAXPOS, SPLIT)
+        dT = hip.Decoder(m, p, T, PPS, MAXPOS, SPLIT)
+        dev = HipStepDevice(d1, dT)
+        toks, pages = _generate(dev, p, T)
+        assert dev._prefill is not None
+        assert toks == want_toks
+        assert pages == want_pages
+        for i, (l, s) in enumerate((l, s) for l in range(CFG["n_layers"]) for s in (0, 1)):
+            assert np.array_equal(p.pages(s, l).view(np.uint16).ravel(), want_slabs[i].ravel()), (l, s)
