@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 
 # attention split per workload (the split fixes the canonical reduction order, so it is a
 # decoder parameter): the largest that still gives every resident wave several items
-SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256}
+SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256, "prefill5": 256}
 
 WORKLOADS = {
     # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
@@ -120,6 +120,76 @@ def attention_workload(args) -> dict:
     return out
 
 
+# bulk prefill workloads: (model, tile rows T, prompt tokens, seed)
+PREFILL_WORKLOADS = {"prefill5": ("llama3_8b", 512, 4096, 6)}
+
+
+def prefill_workload(args) -> dict:
+    """Bulk paged prefill (prefill-range!, paged_decoder.clj:638-711): a step is one
+    4096-token prompt of a Llama-3-8B-shaped Q4 model written into a fresh route of
+    permuted pages, ``T`` rows per tile through ``rstr_prefill_range`` (layers only).
+    Each tile's rows are causal lanes: projections run as one M = T MFMA tile per
+    linear, attention reads the route's pages up to each row."""
+    name, T, P, seed = PREFILL_WORKLOADS[args.workload]
+    cfg = configs.MODELS[name]
+    ps = 16
+    pps = P // ps
+    rng = np.random.default_rng(seed)
+    sess = hip.Session(0)
+    model = hip.Model(sess, cfg, seed=1)
+    physical = 4 * pps
+    pool = hip.Pool(model, ps, physical)
+    pf = hip.Prefill(model, pool, T, pps, P, args.split)
+    prompts = [rng.integers(0, cfg["vocab"], P).astype(np.int32) for _ in range(4)]
+    tables = [rng.permutation(physical)[:pps].astype(np.int32) for _ in range(4)]
+
+    def prefill(i):
+        toks, pt = prompts[i % 4], tables[i % 4]
+        for t0 in range(0, P, T):
+            pos = np.arange(t0, t0 + T, dtype=np.int32)
+            slots = pt[pos // ps] * ps + pos % ps
+            pf.prefill_range(toks[t0:t0 + T], slots, pos, pt, t0 + T, 0)
+
+    for i in range(args.warmup):
+        prefill(i)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        prefill(i)
+    dt = time.perf_counter() - t0
+    value = args.steps * P / dt
+    d, qd, kvd = cfg["d_model"], cfg["n_q"] * cfg["head_dim"], cfg["n_kv"] * cfg["head_dim"]
+    per_layer = (qd + 2 * kvd) * d + d * qd + 2 * cfg["d_ff"] * d + d * cfg["d_ff"]
+    linear = 2 * per_layer * cfg["n_layers"] * P
+    attn = 4 * cfg["n_q"] * cfg["head_dim"] * cfg["n_layers"] * (P * (P + 1) // 2)
+    tflops = (linear + attn) / (dt / args.steps) / 1e12
+    log(f"{args.workload}: {args.steps} prompts of {P} tokens in {P // T} tiles of {T}: "
+        f"{1e3 * dt / args.steps:.1f} ms/prompt, {value:.0f} tok/s, {tflops:.1f} TFLOP/s algorithmic")
+    out = {
+        "metric": "bulk prefill tokens/sec on 1 MI355X", "value": round(value, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4/int8 block dots exact, fp32 accumulate, fp16 KV",
+        "data": "synthetic (seeded random-init weights, uniform random prompt ids)",
+        "config": {"workload": f"{args.workload}: {name}-shaped Q4 decoder, one {P}-token prompt per step, "
+                               f"prefill tiles of {T} rows (host call per tile, synchronous)",
+                   "prefill_T": T, "prompt": P, "page_size": ps, "attention_split": args.split,
+                   "parallelism": "1 GPU (replica)"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "whole prefill (linear + causal attention flops per prompt / prompt time)"},
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(cfg, prefix=P // 2, budget_s=args.cpu_seconds)
+        except Exception as e:  # the baseline must not hide the GPU number
+            out["cpu_baseline"] = {"error": repr(e)}
+    pf.close()
+    pool.close()
+    model.close()
+    sess.close()
+    return out
+
+
 def cpu_attention_baseline(q, lengths, ps, n_kv, hd, scale, split, budget_s) -> dict:
     """The oracle's routed attention (paged_attention.clj:196-228 restated in C,
     OpenMP over lanes) on host fp16 pages: lanes of the same workload taken in
@@ -197,7 +267,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS))
+    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + sorted(PREFILL_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--pool-fraction", type=float, default=0.8)
     ap.add_argument("--split", type=int, default=None, help="attention split (default: per workload)")
@@ -214,6 +284,9 @@ def main():
 
     if args.workload in ATTN_WORKLOADS:
         print(json.dumps(attention_workload(args)), flush=True)
+        return
+    if args.workload in PREFILL_WORKLOADS:
+        print(json.dumps(prefill_workload(args)), flush=True)
         return
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
     cfg = configs.MODELS[name]

@@ -149,6 +149,26 @@ int rstr_decoder_read_rows(rstr_decoder* d, float* out);
 /* 1 (default): replay each step as one captured HIP graph; 0: launch eagerly. */
 int rstr_decoder_set_graph(rstr_decoder* d, int32_t enabled);
 
+/* ---- bulk paged prefill ----------------------------------------------------
+ * Replaces the :prefill-T half of paged-decoder/open! (the prefill link bound
+ * with :include-head-tail? false, paged_decoder.clj:380-405; per-layer
+ * prefill stages decoder_gpu.clj:729-760, 1047-1053): a decoder over `rows`
+ * tile rows of one route, layers only -- no head, no tail, no tokens, and the
+ * decode decoder's resident input rows are left alone.  rstr_step_lanes and
+ * schedules reject it. */
+int rstr_prefill_open(rstr_model* m, rstr_pool* p, int32_t rows, int32_t pages_per_seq,
+                      int32_t maxpos, int32_t split, rstr_decoder** out);
+/* Replaces prefill-range!'s upload + gpu-link/run! (paged_decoder.clj:638-711):
+ * tokens[rows], slots[rows] (the range reservation's physical slots, none -1),
+ * positions[rows], the route's page_table[pages_per_seq] (-1 padded), the
+ * route length (all rows included) and its start position.  Row i attends to
+ * [start_position, positions[i]] and appends its K/V at slots[i]; the result
+ * equals priming the same tokens one decode step at a time, bit for bit.
+ * Returns when the tile's K/V are in the pool. */
+int rstr_prefill_range(rstr_decoder* d, const int32_t* tokens, const int32_t* slots,
+                       const int32_t* positions, const int32_t* page_table, int32_t length,
+                       int32_t start_position);
+
 /* ---- isolated routed append -------------------------------------------------
  * Replaces the paged-append runner run! (paged_append.clj:179-339) over the
  * routed append ABI (doc/serving-architecture.md:178-190): f32 rows

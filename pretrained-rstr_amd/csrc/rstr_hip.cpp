@@ -146,6 +146,7 @@ struct rstr_decoder {
   // offsets into desc
   int64_t off_slots = 0, off_rows = 0, off_pos = 0, off_len = 0, off_start = 0, off_pt = 0;
   bool use_graph = true;
+  bool head_tail = true;                            // false: bulk-prefill decoder (layers only)
   hipGraphExec_t graph = nullptr;
   // schedules
   int32_t* sched_desc = nullptr;
@@ -666,8 +667,8 @@ static void decoder_free(rstr_decoder* d) {
   delete d;
 }
 
-extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps, int32_t maxpos,
-                                 int32_t split, rstr_decoder** out) {
+static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps, int32_t maxpos,
+                        int32_t split, bool head_tail, rstr_decoder** out) {
   if (!m || !p) return fail(nullptr, RSTR_E_INVALID, "null model or pool");
   rstr_session* s = m->s;
   if (!out) return fail(s, RSTR_E_INVALID, "null output pointer");
@@ -687,6 +688,7 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   d->pps = pps;
   d->maxpos = maxpos;
   d->split = split;
+  d->head_tail = head_tail;
   d->mpad = (batch + 15) / 16 * 16;
   d->qd = md.n_q * md.head_dim;
   d->kvr = md.n_kv * md.head_dim;
@@ -717,7 +719,7 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   A(dmalloc(&d->yqkv, (size_t)d->s_qkv * batch * d->nqkv));
   A(dmalloc(&d->qr, (size_t)batch * d->qd));
   A(dmalloc(&d->gu, (size_t)d->s_gu * batch * 2 * md.d_ff));
-  A(dmalloc(&d->logits, (size_t)batch * md.vocab));
+  if (head_tail) A(dmalloc(&d->logits, (size_t)batch * md.vocab));
   A(dmalloc(&d->part, (size_t)d->max_items * G * (md.head_dim + 2)));
   A(dmalloc(&d->rope_cos, (size_t)2 * maxpos * half));
   A(dmalloc(&d->rope_sin, (size_t)2 * maxpos * half));
@@ -765,6 +767,17 @@ extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int
   }
   *out = d;
   return RSTR_OK;
+}
+
+extern "C" int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps, int32_t maxpos,
+                                 int32_t split, rstr_decoder** out) {
+  return decoder_open(m, p, batch, pps, maxpos, split, true, out);
+}
+
+extern "C" int rstr_prefill_open(rstr_model* m, rstr_pool* p, int32_t rows, int32_t pps, int32_t maxpos,
+                                 int32_t split, rstr_decoder** out) {
+  if (m && rows > maxpos) return fail(m->s, RSTR_E_INVALID, "prefill-T must fit in maxpos");
+  return decoder_open(m, p, rows, pps, maxpos, split, false, out);
 }
 
 extern "C" int rstr_decoder_close(rstr_decoder* d) {
@@ -981,6 +994,7 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
       return launch_post_ffn(st, Slices{d->o, d->s_down, sd}, d->xmid, d->r0, W.ffn_post_norm, gnext, goff, md.eps, B, dm, d->act);
     });
   }
+  if (!d->head_tail) return e;
   run(RSTR_K_HEAD, [&] {
     return launch_qgemm(st, d->m->head, d->act, B, d->logits, md.vocab, 1, (size_t)B * md.vocab);
   });
@@ -1011,7 +1025,7 @@ static int run_step_device(rstr_decoder* d) {
   } else {
     HIPCHK(s, enqueue_step(d, s->stream, nullptr));
   }
-  d->has_logits = true;
+  d->has_logits = d->head_tail;
   return RSTR_OK;
 }
 
@@ -1020,6 +1034,7 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
                                const int32_t* start_positions, int32_t* tokens_out) {
   if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
   rstr_session* s = d->m->s;
+  if (!d->head_tail) return fail(s, RSTR_E_STATE, "a bulk-prefill decoder has no head; use rstr_prefill_range");
   int rc = validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions);
   if (rc) return rc;
   if (!tokens_out) return fail(s, RSTR_E_INVALID, "null token output");
@@ -1035,12 +1050,49 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
   return RSTR_OK;
 }
 
+// One complete tile of `rows` prompt tokens of one route: row i is a causal
+// lane whose visible range is [start, positions[i]] of the same page-table row,
+// so every row's attention and projections follow the decode step's reduction
+// order and the K/V written equal token-by-token priming bit for bit.
+extern "C" int rstr_prefill_range(rstr_decoder* d, const int32_t* tokens, const int32_t* slots,
+                                  const int32_t* positions, const int32_t* page_table, int32_t length,
+                                  int32_t start_position) {
+  if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
+  rstr_session* s = d->m->s;
+  if (d->head_tail) return fail(s, RSTR_E_STATE, "Paged decoder has no resident bulk-prefill executable");
+  if (!tokens || !slots || !positions || !page_table) return fail(s, RSTR_E_INVALID, "null descriptor");
+  const int T = d->B;
+  std::vector<int32_t> rows(T + 1), len(T), start(T, start_position), pt((size_t)T * d->pps), lanes(T);
+  for (int i = 0; i < T; i++) {
+    if (tokens[i] < 0 || tokens[i] >= d->m->d.vocab) return fail(s, RSTR_E_INVALID, "token id out of range");
+    int64_t L = (int64_t)positions[i] - start_position + 1;
+    if (L < 1 || L > length) return fail(s, RSTR_E_INVALID, "prefill row position outside the route");
+    len[i] = (int32_t)L;
+    rows[i] = i;
+    lanes[i] = i;
+    std::memcpy(pt.data() + (size_t)i * d->pps, page_table, sizeof(int32_t) * d->pps);
+  }
+  rows[T] = T;
+  int rc = validate_step(d, slots, rows.data(), positions, pt.data(), len.data(), start.data());
+  if (rc) return rc;
+  for (int i = 0; i < T; i++)
+    if (slots[i] < 0) return fail(s, RSTR_E_INVALID, "every prefill row appends its K/V");
+  if ((rc = rstr_prime_lanes(d, T, lanes.data(), tokens))) return rc;
+  pack_desc(d, d->h_desc, slots, rows.data(), positions, pt.data(), len.data(), start.data());
+  HIPCHK(s, hipMemcpyAsync(d->desc, d->h_desc, sizeof(int32_t) * d->desc_words, hipMemcpyHostToDevice,
+                           s->stream));
+  if ((rc = run_step_device(d))) return rc;
+  HIPCHK(s, hipStreamSynchronize(s->stream));
+  return RSTR_OK;
+}
+
 // ---------------------------------------------------------------------------
 // schedules (measurement)
 // ---------------------------------------------------------------------------
 extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* steps, int32_t n) {
   if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
   rstr_session* s = d->m->s;
+  if (!d->head_tail) return fail(s, RSTR_E_STATE, "schedules replay decode steps, not prefill tiles");
   if (n <= 0 || !steps) return fail(s, RSTR_E_INVALID, "empty schedule");
   int64_t words = 0, pages = 0;
   uint64_t fill_seed = 0;

@@ -27,7 +27,8 @@ EXPORTS = (
     "rstr_model_export_linear", "rstr_pool_open", "rstr_pool_close", "rstr_pool_copy_page",
     "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_decoder_open",
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
-    "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_append_run",
+    "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_prefill_open",
+    "rstr_prefill_range", "rstr_append_run",
     "rstr_attention_run",
     "rstr_attention_bench", "rstr_schedule_upload", "rstr_schedule_run",
     "rstr_decoder_profile_steps",
@@ -99,6 +100,8 @@ def lib():
             "rstr_decode_logits": (i32, [P, P]),
             "rstr_decoder_read_rows": (i32, [P, P]),
             "rstr_decoder_set_graph": (i32, [P, i32]),
+            "rstr_prefill_open": (i32, [P, P, i32, i32, i32, i32, C.POINTER(P)]),
+            "rstr_prefill_range": (i32, [P, P, P, P, P, i32, i32]),
             "rstr_append_run": (i32, [P, i32, i32, P, P, P]),
             "rstr_attention_run": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, P, P, i32, P, P, P]),
             "rstr_attention_bench": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, i32, P, i32,
@@ -160,7 +163,7 @@ class Session:
 
     def close(self):
         if self.h:
-            order = {"Decoder": 0, "Pool": 1, "Model": 2}
+            order = {"Decoder": 0, "Prefill": 0, "Pool": 1, "Model": 2}
             for obj in sorted(self.children, key=lambda o: order.get(type(o).__name__, 3)):
                 obj.close()
             self.children = []
@@ -384,6 +387,44 @@ class Decoder:
         n = np.zeros(len(KERNEL_CLASSES), np.int32)
         self.sess.check(lib().rstr_decoder_profile_steps(self.h, first, count, _p(ms), _p(n)))
         return {k: (float(ms[i]), int(n[i])) for i, k in enumerate(KERNEL_CLASSES)}
+
+    def close(self):
+        if self.h:
+            lib().rstr_decoder_close(self.h)
+            self.h = None
+
+
+class Prefill:
+    """Bulk-prefill decoder over ``rows`` tile rows (the ``:prefill-T`` link of
+    paged-decoder/open!, layers only) and prefill-range!'s run."""
+
+    def __init__(self, model: Model, pool: Pool, rows: int, pages_per_seq: int, maxpos: int,
+                 split: int = 256):
+        self.model, self.pool, self.sess = model, pool, model.sess
+        self.rows, self.pps, self.maxpos, self.split = rows, pages_per_seq, maxpos, split
+        h = C.c_void_p()
+        self.sess.check(lib().rstr_prefill_open(model.h, pool.h, rows, pages_per_seq, maxpos, split,
+                                                C.byref(h)))
+        self.h = h
+        self.sess._adopt(self)
+
+    def set_graph(self, enabled: bool):
+        self.sess.check(lib().rstr_decoder_set_graph(self.h, 1 if enabled else 0))
+
+    def prefill_range(self, tokens, slots, positions, page_table, length: int, start_position: int):
+        tokens, slots, positions, page_table = (_i32(a).ravel() for a in (tokens, slots, positions, page_table))
+        if tokens.size != self.rows or slots.size != self.rows or positions.size != self.rows:
+            raise ValueError("Prompt tile does not match the bound prefill row count")
+        if page_table.size != self.pps:
+            raise ValueError("page table row does not match pages_per_seq")
+        self.sess.check(lib().rstr_prefill_range(self.h, _p(tokens), _p(slots), _p(positions),
+                                                 _p(page_table), int(length), int(start_position)))
+
+    def rows_out(self) -> np.ndarray:
+        """The tile's final hidden rows [rows][d_model] (before the head)."""
+        out = np.empty((self.rows, self.model.cfg["d_model"]), np.float32)
+        self.sess.check(lib().rstr_decoder_read_rows(self.h, _p(out)))
+        return out
 
     def close(self):
         if self.h:

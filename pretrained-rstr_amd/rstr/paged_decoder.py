@@ -17,44 +17,15 @@ from . import paged_append
 from .page_pool import PagePool, PagePoolError
 
 
-def prefill_lane_descriptors(desc: dict, batch: int) -> dict:
-    """A bulk-prefill tile of one route (T rows, ``row_offsets`` [0, T]) as the
-    decode step's per-lane descriptors: row t becomes lane t with the route's
-    page-table row, its own append slot and position, and the causal length
-    ``position - start + 1``.  Every row's arithmetic is then exactly the decode
-    step's for that token (the kernels' reduction orders are per row), and the
-    projections run as one M = T tile through the MFMA path."""
-    tokens = np.asarray(desc["tokens"], np.int32)
-    T = tokens.size
-    if T > batch:
-        raise PagePoolError("Prefill tile exceeds the bound prefill lanes", prefill_T=T, lanes=batch)
-    row = np.asarray(desc["page_table"], np.int32).ravel()
-    start = int(np.asarray(desc["start_positions"]).ravel()[0])
-    pos = np.asarray(desc["positions"], np.int32)
-    slots = np.full(batch, -1, np.int32)
-    slots[:T] = desc["slots"]
-    positions = np.zeros(batch, np.int32)
-    positions[:T] = pos
-    lengths = np.zeros(batch, np.int32)
-    lengths[:T] = pos - start + 1
-    starts = np.zeros(batch, np.int32)
-    starts[:T] = start
-    pt = np.full((batch, row.size), -1, np.int32)
-    pt[:T] = row
-    return {"slots": slots, "row_offsets": np.arange(batch + 1, dtype=np.int32), "positions": positions,
-            "page_table": pt.ravel(), "lengths": lengths, "start_positions": starts,
-            "lanes": np.arange(T, dtype=np.int32), "tokens": tokens}
-
-
 class HipStepDevice:
     """Adapter from the three-call device protocol to one ``rstr_step_lanes`` call
     (which uploads, replays the step graph and downloads the tokens).  With a
-    ``prefill_decoder`` (a second decoder whose lanes are the tile rows, on the
-    same model and pool) it also runs bulk-prefill tiles."""
+    ``prefill`` (``hip.Prefill`` on the same model and pool) it also runs
+    bulk-prefill tiles through ``rstr_prefill_range``."""
 
-    def __init__(self, decoder, prefill_decoder=None):
+    def __init__(self, decoder, prefill=None):
         self.decoder = decoder
-        self.prefill_decoder = prefill_decoder
+        self.prefill = prefill
         self._desc = None
         self._tokens = None
         self._prefill = None
@@ -73,14 +44,15 @@ class HipStepDevice:
             self.decoder.prime_lanes([lt["lane"] for lt in lane_tokens], [lt["token"] for lt in lane_tokens])
 
     def upload_prefill(self, desc: dict):
-        if self.prefill_decoder is None:
+        if self.prefill is None:
             raise PagePoolError("Paged decoder has no resident bulk-prefill executable")
-        self._prefill = prefill_lane_descriptors(desc, self.prefill_decoder.batch)
+        self._prefill = desc
 
     def run_prefill(self):
         d = self._prefill
-        self.prefill_decoder.prime_lanes(d["lanes"], d["tokens"])
-        self.prefill_decoder.step_lanes(**{k: d[k] for k in DESCRIPTOR_KEYS})
+        self.prefill.prefill_range(d["tokens"], d["slots"], d["positions"], d["page_table"],
+                                   int(np.asarray(d["lengths"]).ravel()[0]),
+                                   int(np.asarray(d["start_positions"]).ravel()[0]))
 
 
 DESCRIPTOR_KEYS = ("slots", "row_offsets", "positions", "page_table", "lengths", "start_positions")

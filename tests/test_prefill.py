@@ -6,8 +6,9 @@ priming bit for bit: the same K/V in every page of every layer and the same
 generated tokens.
 
 - CPU: the oracle decoder with prefill tiles vs the oracle decoding token by token.
-- GPU: the HIP decoders (a 1-lane decode decoder and a T-lane prefill decoder on
-  one pool) vs the oracle decoding token by token.
+- GPU: the HIP decode decoder (1 lane) and prefill decoder (``rstr_prefill_range``
+  over T rows, layers only) on one pool vs the oracle decoding token by token;
+  the prefill decoder's error paths.
 """
 import numpy as np
 import pytest
@@ -15,13 +16,37 @@ import pytest
 import oracle as O
 from rstr import configs, hip
 from rstr.page_pool import PagePool
-from rstr.paged_decoder import PagedDecoder, HipStepDevice, prefill_lane_descriptors, DESCRIPTOR_KEYS
+from rstr.paged_decoder import PagedDecoder, HipStepDevice, DESCRIPTOR_KEYS
 
 CFG = configs.MODELS["tiny_llama"]
 PS, PAGES, MAXPOS, SPLIT, SEED, T = 16, 40, 160, 32, 9, 24
 PPS = MAXPOS // PS
 PROMPT = [int(x) for x in np.random.default_rng(3).integers(0, CFG["vocab"], 61)]
 MAX_NEW = 5
+
+
+def prefill_lane_descriptors(desc: dict, batch: int) -> dict:
+    """A bulk-prefill tile of one route (T rows, ``row_offsets`` [0, T]) as
+    decode-step lanes, the way ``rstr_prefill_range`` runs it: row t becomes
+    lane t with the route's page-table row, its own slot and position, and the
+    causal length ``position - start + 1``."""
+    tokens = np.asarray(desc["tokens"], np.int32)
+    T = tokens.size
+    assert T <= batch
+    row = np.asarray(desc["page_table"], np.int32).ravel()
+    start = int(np.asarray(desc["start_positions"]).ravel()[0])
+    pos = np.asarray(desc["positions"], np.int32)
+    out = {"slots": np.full(batch, -1, np.int32), "row_offsets": np.arange(batch + 1, dtype=np.int32),
+           "positions": np.zeros(batch, np.int32), "page_table": np.full((batch, row.size), -1, np.int32),
+           "lengths": np.zeros(batch, np.int32), "start_positions": np.zeros(batch, np.int32),
+           "lanes": np.arange(T, dtype=np.int32), "tokens": tokens}
+    out["slots"][:T] = desc["slots"]
+    out["positions"][:T] = pos
+    out["lengths"][:T] = pos - start + 1
+    out["start_positions"][:T] = start
+    out["page_table"][:T] = row
+    out["page_table"] = out["page_table"].ravel()
+    return out
 
 
 def _pad_lanes(desc, batch):
@@ -126,11 +151,36 @@ def test_gpu_prefill_tiles_equal_oracle_token_by_token():
         m = hip.Model(sess, CFG, seed=SEED)
         p = hip.Pool(m, PS, PAGES)
         d1 = hip.Decoder(m, p, 1, PPS, MAXPOS, SPLIT)
-        dT = hip.Decoder(m, p, T, PPS, MAXPOS, SPLIT)
-        dev = HipStepDevice(d1, dT)
+        pf = hip.Prefill(m, p, T, PPS, MAXPOS, SPLIT)
+        dev = HipStepDevice(d1, pf)
         toks, pages = _generate(dev, p, T)
         assert dev._prefill is not None
         assert toks == want_toks
         assert pages == want_pages
         for i, (l, s) in enumerate((l, s) for l in range(CFG["n_layers"]) for s in (0, 1)):
             assert np.array_equal(p.pages(s, l).view(np.uint16).ravel(), want_slabs[i].ravel()), (l, s)
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_decoder_rejects_decode_calls_and_bad_tiles():
+    print("case prefill errors", flush=True)
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=SEED)
+        p = hip.Pool(m, PS, PAGES)
+        pf = hip.Prefill(m, p, 4, PPS, MAXPOS, SPLIT)
+        z = np.zeros(4, np.int32)
+        descs = [np.ascontiguousarray(a, np.int32) for a in (z - 1, np.arange(5), z, np.full(4 * PPS, -1), z, z, z)]
+        with pytest.raises(hip.RstrError, match="no head"):
+            sess.check(hip.lib().rstr_step_lanes(pf.h, *[a.ctypes.data for a in descs]))
+        row = np.full(PPS, -1, np.int32)
+        row[0] = 3
+        # a row outside the route, and a slot that is not the row's own token
+        with pytest.raises(hip.RstrError, match="outside the route"):
+            pf.prefill_range([1, 2, 3, 4], [48, 49, 50, 51], [0, 1, 2, 3], row, 3, 0)
+        with pytest.raises(hip.RstrError, match="slot"):
+            pf.prefill_range([1, 2, 3, 4], [48, 49, 51, 50], [0, 1, 2, 3], row, 4, 0)
+        with pytest.raises(hip.RstrError, match="prefill-T"):
+            hip.Prefill(m, p, MAXPOS + 1, PPS, MAXPOS, SPLIT)
+        pf.prefill_range([1, 2, 3, 4], [48, 49, 50, 51], [0, 1, 2, 3], row, 4, 0)
+        with pytest.raises(hip.RstrError, match="schedules"):
+            sess.check(hip.lib().rstr_schedule_upload(pf.h, None, 1))
