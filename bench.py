@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 
 # attention split per workload (the split fixes the canonical reduction order, so it is a
 # decoder parameter): the largest that still gives every resident wave several items
-SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256, "prefill5": 256}
+SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256, "prefill5": 256, "chunk5": 256}
 
 WORKLOADS = {
     # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
@@ -190,6 +190,106 @@ def prefill_workload(args) -> dict:
     return out
 
 
+# durable chunk workloads: (model, chunk tokens, route pages, seed)
+CHUNK_WORKLOADS = {"chunk5": ("llama3_8b", 4096, 320, 7)}
+
+
+def chunk_workload(args) -> dict:
+    """KV chunk export/restore (page_pool.clj:1111-1374): a 4096-token durable
+    chunk of a Llama-3-8B-shaped fp16 pool (32 layers x K/V, 2 KiB rows: 512 MiB
+    payload) starting 5 tokens into a route of permuted pages.  ``value`` is the
+    export rate through the C ABI, payload bytes over the transfer's device time
+    (page list copy + gather kernel + device-to-host DMA into pinned memory);
+    the roofline is the gather kernel alone (HBM: the payload read from pages
+    and written to staging)."""
+    name, T, npages, seed = CHUNK_WORKLOADS[args.workload]
+    cfg = configs.MODELS[name]
+    ps = 16
+    rng = np.random.default_rng(seed)
+    sess = hip.Session(0)
+    model = hip.Model(sess, cfg, seed=1)
+    physical = 4 * npages
+    pool = hip.Pool(model, ps, physical)
+    pool.fill_synthetic(np.arange(physical, dtype=np.int32), seed)
+    pages = rng.permutation(physical)[:npages].astype(np.int32)
+    start = 5
+    payload_bytes = pool.chunk_elements(T) * 2
+    ex = [None]
+
+    def export():
+        st = pool.export_submit(pages, start, T).complete()
+        ex[0] = st["payload"]
+        return st["device_ms"]
+
+    for _ in range(max(1, args.warmup)):
+        export()
+    t0 = time.perf_counter()
+    dev = [export() for _ in range(args.steps)]
+    wall = (time.perf_counter() - t0) / args.steps
+    exp_ms = float(np.median(dev))
+    other = np.setdiff1d(np.arange(physical), pages)[:npages].astype(np.int32)
+    rdev = [pool.restore_submit(other, start, T, ex[0]).complete()["device_ms"] for _ in range(max(2, args.steps // 2))]
+    res_ms = float(np.median(rdev))
+    iters = max(10, args.steps)
+    g_ms = pool.chunk_bench(pages, start, T, 0, iters)
+    s_ms = pool.chunk_bench(other, start, T, 1, iters)
+    gbs = payload_bytes / (exp_ms * 1e-3) / 1e9
+    kern_gbs = 2 * payload_bytes / (g_ms * 1e-3) / 1e9
+    log(f"{args.workload}: {T}-token chunk, {payload_bytes / 2**20:.0f} MiB: export {exp_ms:.2f} ms device "
+        f"({gbs:.1f} GB/s, wall {1e3 * wall:.2f} ms), restore {res_ms:.2f} ms "
+        f"({payload_bytes / (res_ms * 1e-3) / 1e9:.1f} GB/s); gather kernel {1e3 * g_ms:.1f} us "
+        f"({kern_gbs:.0f} GB/s HBM), scatter kernel {1e3 * s_ms:.1f} us")
+    out = {
+        "metric": "durable KV chunk export GB/s (payload bytes / device time) on 1 MI355X",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(exp_ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 KV rows", "data": "synthetic (seeded fp16 page templates)",
+        "config": {"workload": f"{args.workload}: {name}-shaped fp16 pool, one {T}-token chunk starting 5 tokens into "
+                               f"a route of {npages} permuted 16-token pages; export = page list + gather kernel + "
+                               "DMA to pinned host memory",
+                   "chunk_tokens": T, "payload_bytes": payload_bytes, "page_size": ps,
+                   "parallelism": "1 GPU (replica)"},
+        "restore": {"device_ms": round(res_ms, 3), "gbs": round(payload_bytes / (res_ms * 1e-3) / 1e9, 2)},
+        "export_wall_ms": round(1e3 * wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_chunk_move<0> (gather; payload read from pages + written to staging)",
+                     "bytes_per_launch": 2 * payload_bytes, "avg_launch_ms": round(g_ms, 4),
+                     "scatter_avg_launch_ms": round(s_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_chunk_baseline(cfg, T, args.cpu_seconds)
+        except Exception as e:  # the baseline must not hide the GPU number
+            out["cpu_baseline"] = {"error": repr(e)}
+    pool.close()
+    model.close()
+    sess.close()
+    return out
+
+
+def cpu_chunk_baseline(cfg, T, budget_s) -> dict:
+    """The oracle's chunk gather (numpy fancy indexing over host slabs) on a
+    1/8 sample of the chunk's tokens, all layers."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import chunk_oracle as OC  # checker / CPU baseline only
+    ps, n = 16, T // 8
+    ept = cfg["n_kv"] * cfg["head_dim"]
+    npg = -(-(n + 5) // ps)
+    rng = np.random.default_rng(3)
+    slabs = [rng.integers(0, 2**15, (4 * npg * ps, ept)).astype(np.uint16) for _ in range(2 * cfg["n_layers"])]
+    pages = rng.permutation(4 * npg)[:npg]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        out = OC.gather(slabs, pages, ps, 5, n)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(out.nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} of {T} tokens, all {2 * cfg['n_layers']} slab-layers, {reps} gathers"}
+
+
 def cpu_attention_baseline(q, lengths, ps, n_kv, hd, scale, split, budget_s) -> dict:
     """The oracle's routed attention (paged_attention.clj:196-228 restated in C,
     OpenMP over lanes) on host fp16 pages: lanes of the same workload taken in
@@ -267,7 +367,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + sorted(PREFILL_WORKLOADS))
+    ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + sorted(PREFILL_WORKLOADS)
+                    + sorted(CHUNK_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--pool-fraction", type=float, default=0.8)
     ap.add_argument("--split", type=int, default=None, help="attention split (default: per workload)")
@@ -287,6 +388,9 @@ def main():
         return
     if args.workload in PREFILL_WORKLOADS:
         print(json.dumps(prefill_workload(args)), flush=True)
+        return
+    if args.workload in CHUNK_WORKLOADS:
+        print(json.dumps(chunk_workload(args)), flush=True)
         return
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
     cfg = configs.MODELS[name]

@@ -32,6 +32,7 @@ typedef struct rstr_session rstr_session;
 typedef struct rstr_model rstr_model;
 typedef struct rstr_pool rstr_pool;
 typedef struct rstr_decoder rstr_decoder;
+typedef struct rstr_transfer rstr_transfer;
 
 /* Descriptor flags of src/pretrained/arch/{gemma3,qwen3,llama}.clj plus the HF
  * hyper-parameters read by decoder.clj:31-56 (load-hf). */
@@ -115,6 +116,50 @@ int rstr_pool_download(rstr_pool* p, int32_t slab, int32_t layer, int64_t src_el
  * (seed, layer, slab, element): the stand-in for a restored prefix used by
  * throughput runs.  No reference counterpart. */
 int rstr_pool_fill_synthetic(rstr_pool* p, const int32_t* pages, int32_t n_pages, uint64_t seed);
+
+/* ---- durable chunk transfer --------------------------------------------------
+ * A chunk is `token_count` consecutive tokens [start, start + token_count) of a
+ * route whose logical pages are pages[0 .. n_pages).  Its payload is dense in
+ * the portable layout of attention_state.clj:103-123 (payload-plan): the key
+ * slab of layers 0..L-1, then the value slab of layers 0..L-1, each holding
+ * token_count rows of n_kv*head_dim elements, little-endian fp16
+ * (page_pool.clj:1271-1286, :chunk/version 3).  Ranges may start and end inside
+ * pages and cross any physical pages; one gather or scatter kernel covers every
+ * slab and layer, with one DMA copy between pinned host memory and a pool
+ * staging buffer.  A submitted transfer runs on the session stream (ordered
+ * after earlier steps and copies); the caller keeps `payload` alive and the
+ * route's pages leased until rstr_transfer_complete, which waits, records the
+ * device time and releases the transfer.  A pool with open transfers refuses
+ * to close. */
+typedef struct rstr_transfer_stats {
+  int64_t bytes;       /* payload bytes moved between host and device       */
+  float device_ms;     /* HIP events around the copy and kernel on the stream */
+  int32_t direction;   /* 0 upload (restore), 1 download (export)            */
+} rstr_transfer_stats;
+/* Replaces submit-export-chunk! (page_pool.clj:1288-1318) and the gather of
+ * export-chunk (:1347-1374): payload receives 2*L*token_count*n_kv*head_dim
+ * fp16 elements on completion. */
+int rstr_chunk_export_submit(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                             int32_t token_count, uint16_t* payload, rstr_transfer** out);
+/* Replaces submit-restore-chunk! (page_pool.clj:1169-1184) and restore-chunk!
+ * (:1211-1224): payload_dtype 0 = fp16 elements, 1 = f32 elements rounded to
+ * fp16 to nearest even (half-payload, :1084-1109). */
+int rstr_chunk_restore_submit(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                              int32_t token_count, const void* payload, int32_t payload_dtype,
+                              rstr_transfer** out);
+/* Replaces chunk-transfer-complete? / chunk-export-complete? (:1186-1193,
+ * :1320-1327): 1 when the device work is done, 0 while pending. */
+int rstr_transfer_done(rstr_transfer* t);
+/* Replaces complete-restore-chunk! / complete-export-chunk! (:1195-1209,
+ * :1329-1345): waits, fills `stats` (may be NULL) and frees the transfer. */
+int rstr_transfer_complete(rstr_transfer* t, rstr_transfer_stats* stats);
+/* Measurement only, no reference counterpart: the average device time of the
+ * chunk gather (mode 0) or fp16 scatter (mode 1) kernel alone, between the pool
+ * and its device staging (no host copies), over `iters` launches timed with
+ * HIP events on the session stream.  Scatter overwrites the chunk's tokens
+ * with whatever the staging holds. */
+int rstr_chunk_bench(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                     int32_t token_count, int32_t mode, int32_t iters, float* kernel_ms);
 
 /* ---- paged decoder ----------------------------------------------------------
  * Replaces paged-decoder/open! (paged_decoder.clj:321-420) over a state bound

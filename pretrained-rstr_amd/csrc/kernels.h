@@ -115,6 +115,9 @@ hipError_t launch_append_rows(hipStream_t st, const float* k_rows, const float* 
                               int kvr, const int32_t* slots, uint16_t* kpages, uint16_t* vpages);
 hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64_t page_elems,
                              const int32_t* pairs, int npairs);
+// mode 0: pool -> fp16 payload; 1: fp16 payload -> pool; 2: f32 payload -> pool (RNE)
+hipError_t launch_chunk_move(hipStream_t st, int mode, uint16_t** slabs, int nslabs, const int32_t* pages,
+                             int start, int count, int page_size, int ept, void* payload);
 #define RSTR_SYNTH_TEMPLATES 64
 hipError_t launch_gen_templates(hipStream_t st, uint16_t* tmpl, int n_layers, int64_t page_elems,
                                 uint64_t seed);

@@ -1773,6 +1773,65 @@ hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64
   return hipGetLastError();
 }
 
+// Durable chunk transfer: token rows between the page pool and a dense payload
+// in the portable layout (page_pool.clj:1111-1374; payload order of
+// attention_state.clj:103-123: slab K then V, layer, token; a row is `ept`
+// fp16).  One thread moves one 16-byte piece of one row of one slab-layer;
+// consecutive threads take consecutive pieces of a row, so both sides are
+// coalesced whatever the page table looks like.  Mode 0 gathers pool ->
+// payload, mode 1 scatters an fp16 payload, mode 2 scatters an f32 payload
+// rounded to fp16 (round to nearest even, Float/floatToFloat16).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_chunk_move(uint16_t* const* __restrict__ slabs,
+                                                    const int32_t* __restrict__ pages, int start,
+                                                    int count, int page_size, int ept,
+                                                    int64_t n_pieces, void* __restrict__ payload) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_pieces) return;
+  const int pieces = ept >> 3;
+  const int piece = (int)(i % pieces);
+  const int64_t r = i / pieces;             // (slab-layer, token) row of the payload
+  const int t = (int)(r % count);
+  const int sl = (int)(r / count);
+  const int logical = start + t;
+  const int64_t phys = (int64_t)pages[logical / page_size] * page_size + logical % page_size;
+  uint16_t* row = slabs[sl] + phys * ept + piece * 8;
+  const int64_t off = r * ept + piece * 8;
+  if constexpr (MODE == 0) {
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(payload) + off) = *reinterpret_cast<const u32x4*>(row);
+  } else if constexpr (MODE == 1) {
+    *reinterpret_cast<u32x4*>(row) = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(payload) + off);
+  } else {
+    const float* src = static_cast<const float*>(payload) + off;
+    const f4 a = *reinterpret_cast<const f4*>(src);
+    const f4 b = *reinterpret_cast<const f4*>(src + 4);
+    h8 h;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      h[k] = (_Float16)a[k];
+      h[4 + k] = (_Float16)b[k];
+    }
+    *reinterpret_cast<h8*>(row) = h;
+  }
+}
+
+hipError_t launch_chunk_move(hipStream_t st, int mode, uint16_t** slabs, int nslabs, const int32_t* pages,
+                             int start, int count, int page_size, int ept, void* payload) {
+  if (count <= 0) return hipSuccess;
+  if (ept % 8) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)nslabs * count * (ept / 8);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (mode == 0)
+    hipLaunchKernelGGL(k_chunk_move<0>, grid, dim3(256), 0, st, slabs, pages, start, count, page_size, ept, n, payload);
+  else if (mode == 1)
+    hipLaunchKernelGGL(k_chunk_move<1>, grid, dim3(256), 0, st, slabs, pages, start, count, page_size, ept, n, payload);
+  else if (mode == 2)
+    hipLaunchKernelGGL(k_chunk_move<2>, grid, dim3(256), 0, st, slabs, pages, start, count, page_size, ept, n, payload);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 // Synthetic K/V, the stand-in for a restored prefix.  For each (layer, slab)
 // RSTR_SYNTH_TEMPLATES page templates hold fp16(Irwin-Hall(12) N(0,1)) values
 // keyed by (seed, layer, slab) and (template*page_elems + element); physical

@@ -93,6 +93,24 @@ struct rstr_pool {
   uint16_t* tmpl = nullptr;               // synthetic-prefix page templates
   uint64_t tmpl_seed = 0;
   bool tmpl_ready = false;
+  // durable chunk transfers: dense payload staging and the route's page list
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
+  int32_t* d_chunk_pages = nullptr;
+  int chunk_pages_cap = 0;
+  int open_transfers = 0;
+  std::vector<std::pair<void*, size_t>> pinned;  // idle pinned transfer buffers, reused
+};
+
+struct rstr_transfer {
+  rstr_pool* p = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  void* host = nullptr;          // pinned: page list, then the payload
+  size_t host_bytes = 0;
+  uint16_t* user_dst = nullptr;  // export destination
+  size_t payload_bytes = 0;
+  size_t host_payload_offset = 0;
+  int direction = 0;             // 0 restore (upload), 1 export (download)
 };
 
 // Generate (once per seed) the page templates the synthetic fill copies from.
@@ -568,6 +586,7 @@ extern "C" int rstr_pool_open(rstr_model* m, int32_t page_size, int32_t physical
 
 extern "C" int rstr_pool_close(rstr_pool* p) {
   if (!p) return RSTR_OK;
+  if (p->open_transfers > 0) return fail(p->m->s, RSTR_E_STATE, "pool has chunk transfers in flight");
   hipSetDevice(p->m->s->device);
   hipStreamSynchronize(p->m->s->stream);
   for (auto* q : p->slabs) hipFree(q);
@@ -575,7 +594,190 @@ extern "C" int rstr_pool_close(rstr_pool* p) {
   hipFree(p->d_pairs);
   hipHostFree(p->h_pairs);
   if (p->tmpl) hipFree(p->tmpl);
+  if (p->stage) hipFree(p->stage);
+  if (p->d_chunk_pages) hipFree(p->d_chunk_pages);
+  for (auto& b : p->pinned) hipHostFree(b.first);
   delete p;
+  return RSTR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// durable chunk transfer
+// ---------------------------------------------------------------------------
+// Keep up to 4 idle pinned buffers per pool (the largest), free the rest.
+static void pinned_release(rstr_pool* p, void* host, size_t bytes) {
+  p->pinned.emplace_back(host, bytes);
+  if (p->pinned.size() > 4) {
+    auto smallest = std::min_element(p->pinned.begin(), p->pinned.end(),
+                                      [](const auto& a, const auto& b) { return a.second < b.second; });
+    hipHostFree(smallest->first);
+    p->pinned.erase(smallest);
+  }
+}
+
+static int chunk_submit(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start, int32_t count,
+                        int mode, const void* src, uint16_t* dst, rstr_transfer** out) {
+  if (!p) return fail(nullptr, RSTR_E_INVALID, "null pool");
+  rstr_session* s = p->m->s;
+  if (!out) return fail(s, RSTR_E_INVALID, "null output pointer");
+  *out = nullptr;
+  if (!pages || n_pages <= 0) return fail(s, RSTR_E_INVALID, "empty page list");
+  if (start < 0 || count <= 0 || (int64_t)start + count > (int64_t)n_pages * p->page_size)
+    return fail(s, RSTR_E_INVALID, "Chunk range is outside the resident continuation");
+  const int first = start / p->page_size, last = (start + count - 1) / p->page_size;
+  for (int i = first; i <= last; i++)
+    if (pages[i] < 0 || pages[i] >= p->physical_pages) return fail(s, RSTR_E_INVALID, "page id out of range");
+  if ((mode == 0 && !dst) || (mode != 0 && !src)) return fail(s, RSTR_E_INVALID, "null payload");
+  const auto& md = p->m->d;
+  const int L = md.n_layers, ept = md.n_kv * md.head_dim;
+  const size_t elems = (size_t)2 * L * count * ept;
+  const size_t pbytes = elems * (mode == 2 ? 4 : 2);
+  HIPCHK(s, hipSetDevice(s->device));
+  // grow the pool-owned staging (the stream drains first: earlier transfers use it)
+  if (p->stage_bytes < pbytes || p->chunk_pages_cap < n_pages) {
+    HIPCHK(s, hipStreamSynchronize(s->stream));
+    if (p->stage_bytes < pbytes) {
+      if (p->stage) hipFree(p->stage);
+      p->stage = nullptr;
+      p->stage_bytes = 0;
+      if (hipMalloc(&p->stage, pbytes) != hipSuccess) return fail(s, RSTR_E_OOM, "chunk staging allocation failed");
+      p->stage_bytes = pbytes;
+    }
+    if (p->chunk_pages_cap < n_pages) {
+      if (p->d_chunk_pages) hipFree(p->d_chunk_pages);
+      p->d_chunk_pages = nullptr;
+      p->chunk_pages_cap = 0;
+      if (dmalloc(&p->d_chunk_pages, (size_t)n_pages) != hipSuccess)
+        return fail(s, RSTR_E_OOM, "chunk page list allocation failed");
+      p->chunk_pages_cap = n_pages;
+    }
+  }
+  auto t = std::make_unique<rstr_transfer>();
+  t->p = p;
+  t->direction = mode == 0 ? 1 : 0;
+  t->payload_bytes = pbytes;
+  t->user_dst = dst;
+  const size_t pages_bytes = ((size_t)n_pages * 4 + 255) / 256 * 256;
+  const size_t need = pages_bytes + pbytes;
+  // smallest idle pinned buffer that fits, else a new one
+  int best = -1;
+  for (int i = 0; i < (int)p->pinned.size(); i++)
+    if (p->pinned[i].second >= need && (best < 0 || p->pinned[i].second < p->pinned[best].second)) best = i;
+  if (best >= 0) {
+    t->host = p->pinned[best].first;
+    t->host_bytes = p->pinned[best].second;
+    p->pinned.erase(p->pinned.begin() + best);
+  } else {
+    if (hipHostMalloc(&t->host, need) != hipSuccess) return fail(s, RSTR_E_OOM, "pinned chunk buffer allocation failed");
+    t->host_bytes = need;
+  }
+  auto cleanup = [&]() {
+    if (t->e0) hipEventDestroy(t->e0);
+    if (t->e1) hipEventDestroy(t->e1);
+    pinned_release(p, t->host, t->host_bytes);
+  };
+  std::memcpy(t->host, pages, (size_t)n_pages * 4);
+  t->host_payload_offset = pages_bytes;
+  char* hpay = static_cast<char*>(t->host) + pages_bytes;
+  if (mode != 0) std::memcpy(hpay, src, pbytes);
+  hipError_t e = hipEventCreate(&t->e0);
+  if (e == hipSuccess) e = hipEventCreate(&t->e1);
+  if (e == hipSuccess) e = hipEventRecord(t->e0, s->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p->d_chunk_pages, t->host, (size_t)n_pages * 4, hipMemcpyHostToDevice, s->stream);
+  if (e == hipSuccess && mode != 0) e = hipMemcpyAsync(p->stage, hpay, pbytes, hipMemcpyHostToDevice, s->stream);
+  if (e == hipSuccess)
+    e = launch_chunk_move(s->stream, mode, p->d_slabs, 2 * L, p->d_chunk_pages, start, count, p->page_size, ept,
+                          p->stage);
+  if (e == hipSuccess && mode == 0) e = hipMemcpyAsync(hpay, p->stage, pbytes, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess) e = hipEventRecord(t->e1, s->stream);
+  if (e != hipSuccess) {
+    hipStreamSynchronize(s->stream);
+    cleanup();
+    return fail(s, RSTR_E_HIP, std::string("chunk transfer: ") + hipGetErrorString(e));
+  }
+  p->open_transfers++;
+  *out = t.release();
+  return RSTR_OK;
+}
+
+extern "C" int rstr_chunk_bench(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                                int32_t token_count, int32_t mode, int32_t iters, float* kernel_ms) {
+  if (!p) return fail(nullptr, RSTR_E_INVALID, "null pool");
+  rstr_session* s = p->m->s;
+  if ((mode != 0 && mode != 1) || iters <= 0 || !kernel_ms) return fail(s, RSTR_E_INVALID, "invalid bench request");
+  // a gather submission sets up staging, page list and validation
+  rstr_transfer* t = nullptr;
+  std::vector<uint16_t> sink;
+  if (token_count > 0 && n_pages > 0)
+    sink.resize((size_t)2 * p->m->d.n_layers * token_count * p->m->d.n_kv * p->m->d.head_dim);
+  int rc = chunk_submit(p, pages, n_pages, start, token_count, 0, nullptr, sink.data(), &t);
+  if (rc) return rc;
+  if ((rc = rstr_transfer_complete(t, nullptr))) return rc;
+  const int L = p->m->d.n_layers, ept = p->m->d.n_kv * p->m->d.head_dim;
+  hipEvent_t a, b;
+  HIPCHK(s, hipEventCreate(&a));
+  HIPCHK(s, hipEventCreate(&b));
+  hipError_t e = hipEventRecord(a, s->stream);
+  for (int i = 0; i < iters && e == hipSuccess; i++)
+    e = launch_chunk_move(s->stream, mode, p->d_slabs, 2 * L, p->d_chunk_pages, start, token_count, p->page_size,
+                          ept, p->stage);
+  if (e == hipSuccess) e = hipEventRecord(b, s->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+  hipEventDestroy(a);
+  hipEventDestroy(b);
+  HIPCHK(s, e);
+  *kernel_ms = ms / iters;
+  return RSTR_OK;
+}
+
+extern "C" int rstr_chunk_export_submit(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                                        int32_t token_count, uint16_t* payload, rstr_transfer** out) {
+  return chunk_submit(p, pages, n_pages, start, token_count, 0, nullptr, payload, out);
+}
+
+extern "C" int rstr_chunk_restore_submit(rstr_pool* p, const int32_t* pages, int32_t n_pages, int32_t start,
+                                         int32_t token_count, const void* payload, int32_t payload_dtype,
+                                         rstr_transfer** out) {
+  if (p && payload_dtype != 0 && payload_dtype != 1)
+    return fail(p->m->s, RSTR_E_INVALID, "Payload dtype and representation cannot be restored to FP16");
+  return chunk_submit(p, pages, n_pages, start, token_count, payload_dtype == 1 ? 2 : 1, payload, nullptr, out);
+}
+
+extern "C" int rstr_transfer_done(rstr_transfer* t) {
+  if (!t) return fail(nullptr, RSTR_E_INVALID, "null transfer");
+  hipError_t e = hipEventQuery(t->e1);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  return fail(t->p->m->s, RSTR_E_HIP, std::string("transfer query: ") + hipGetErrorString(e));
+}
+
+extern "C" int rstr_transfer_complete(rstr_transfer* t, rstr_transfer_stats* stats) {
+  if (!t) return fail(nullptr, RSTR_E_INVALID, "null transfer");
+  std::unique_ptr<rstr_transfer> own(t);
+  rstr_pool* p = t->p;
+  rstr_session* s = p->m->s;
+  p->open_transfers--;
+  hipError_t e = hipEventSynchronize(t->e1);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, t->e0, t->e1);
+  if (e == hipSuccess && t->direction == 1) {
+    // the payload follows the 256-byte aligned page list in the pinned buffer
+    const size_t off = t->host_payload_offset;
+    std::memcpy(t->user_dst, static_cast<char*>(t->host) + off, t->payload_bytes);
+  }
+  hipEventDestroy(t->e0);
+  hipEventDestroy(t->e1);
+  if (e == hipSuccess) pinned_release(p, t->host, t->host_bytes);
+  else hipHostFree(t->host);
+  if (e != hipSuccess) return fail(s, RSTR_E_HIP, std::string("transfer completion: ") + hipGetErrorString(e));
+  if (stats) {
+    stats->bytes = (int64_t)t->payload_bytes;
+    stats->device_ms = ms;
+    stats->direction = t->direction;
+  }
   return RSTR_OK;
 }
 

@@ -25,7 +25,8 @@ EXPORTS = (
     "rstr_session_memory",
     "rstr_model_bind", "rstr_model_bind_synthetic", "rstr_model_close", "rstr_model_weight_bytes",
     "rstr_model_export_linear", "rstr_pool_open", "rstr_pool_close", "rstr_pool_copy_page",
-    "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_decoder_open",
+    "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_chunk_export_submit",
+    "rstr_chunk_restore_submit", "rstr_transfer_done", "rstr_transfer_complete", "rstr_chunk_bench", "rstr_decoder_open",
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
     "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_prefill_open",
     "rstr_prefill_range", "rstr_append_run",
@@ -53,6 +54,10 @@ class Desc(C.Structure):
 class Tensor(C.Structure):
     _fields_ = [("layer", C.c_int32), ("role", C.c_int32), ("data", C.c_void_p),
                 ("elements", C.c_int64)]
+
+
+class TransferStats(C.Structure):
+    _fields_ = [("bytes", C.c_int64), ("device_ms", C.c_float), ("direction", C.c_int32)]
 
 
 class StagedStep(C.Structure):
@@ -92,6 +97,11 @@ def lib():
             "rstr_pool_upload": (i32, [P, i32, i32, i64, P, i64]),
             "rstr_pool_download": (i32, [P, i32, i32, i64, P, i64]),
             "rstr_pool_fill_synthetic": (i32, [P, P, i32, u64]),
+            "rstr_chunk_export_submit": (i32, [P, P, i32, i32, i32, P, C.POINTER(P)]),
+            "rstr_chunk_restore_submit": (i32, [P, P, i32, i32, i32, P, i32, C.POINTER(P)]),
+            "rstr_transfer_done": (i32, [P]),
+            "rstr_chunk_bench": (i32, [P, P, i32, i32, i32, i32, i32, C.POINTER(f32)]),
+            "rstr_transfer_complete": (i32, [P, C.POINTER(TransferStats)]),
             "rstr_decoder_open": (i32, [P, P, i32, i32, i32, i32, C.POINTER(P)]),
             "rstr_decoder_close": (i32, [P]),
             "rstr_prime_lanes": (i32, [P, i32, P, P]),
@@ -270,6 +280,48 @@ class Pool:
         self.sess.check(lib().rstr_append_run(self.h, layer, slots.size, _p(k_rows), _p(v_rows),
                                               _p(slots)))
 
+    def chunk_elements(self, token_count: int) -> int:
+        """Payload elements of a durable chunk of ``token_count`` tokens."""
+        c = self.model.cfg
+        return 2 * c["n_layers"] * token_count * c["n_kv"] * c["head_dim"]
+
+    def export_submit(self, pages, start: int, token_count: int) -> "Transfer":
+        """Gather tokens [start, start+token_count) of the route over ``pages`` into a
+        durable fp16 payload (filled when the transfer completes)."""
+        pages = _i32(pages).ravel()
+        out = np.empty(self.chunk_elements(token_count), np.uint16)
+        h = C.c_void_p()
+        self.sess.check(lib().rstr_chunk_export_submit(self.h, _p(pages), pages.size, int(start), int(token_count),
+                                                      _p(out), C.byref(h)))
+        return Transfer(self.sess, h, out, (pages, out))
+
+    def restore_submit(self, pages, start: int, token_count: int, payload) -> "Transfer":
+        """Scatter a durable payload (fp16 bits as uint16, or float32) into the route's pages."""
+        pages = _i32(pages).ravel()
+        payload = np.ascontiguousarray(payload)
+        if payload.dtype == np.float16:
+            payload = payload.view(np.uint16)
+        if payload.dtype == np.uint16:
+            dtype = 0
+        elif payload.dtype == np.float32:
+            dtype = 1
+        else:
+            raise ValueError("Payload dtype and representation cannot be restored to FP16")
+        if payload.size != self.chunk_elements(token_count):
+            raise ValueError("payload length differs from its descriptor")
+        h = C.c_void_p()
+        self.sess.check(lib().rstr_chunk_restore_submit(self.h, _p(pages), pages.size, int(start), int(token_count),
+                                                       _p(payload), dtype, C.byref(h)))
+        return Transfer(self.sess, h, None, (pages, payload))
+
+    def chunk_bench(self, pages, start: int, token_count: int, mode: int, iters: int) -> float:
+        """Average ms of the gather (mode 0) / scatter (mode 1) kernel alone."""
+        pages = _i32(pages).ravel()
+        ms = C.c_float()
+        self.sess.check(lib().rstr_chunk_bench(self.h, _p(pages), pages.size, int(start), int(token_count),
+                                               int(mode), int(iters), C.byref(ms)))
+        return ms.value
+
     def attention(self, layer, q, page_table, lengths, start_positions=None, positions=None,
                   window=0, scale=None, split=256):
         """Isolated routed attention (paged-attention/run!) with f32 q/out."""
@@ -304,9 +356,36 @@ class Pool:
         return a.value, b.value
 
     def close(self):
+        """Frees the slabs; refused (RstrError) while chunk transfers are in flight."""
         if self.h:
-            lib().rstr_pool_close(self.h)
+            self.sess.check(lib().rstr_pool_close(self.h))
             self.h = None
+
+
+class Transfer:
+    """A submitted chunk export/restore; keeps its host buffers alive until completion."""
+
+    def __init__(self, sess: Session, h, payload, retained):
+        self.sess, self.h, self.payload, self._retained = sess, h, payload, retained
+
+    def done(self) -> bool:
+        if self.h is None:  # completed
+            return True
+        rc = lib().rstr_transfer_done(self.h)
+        if rc < 0:
+            self.sess.check(rc)
+        return rc == 1
+
+    def complete(self) -> dict:
+        """Wait, release the transfer; returns {bytes, device_ms, direction, payload}."""
+        if self.h is None:
+            raise RstrError(-4, "transfer already completed")
+        st = TransferStats()
+        h, self.h = self.h, None
+        self.sess.check(lib().rstr_transfer_complete(h, C.byref(st)))
+        self._retained = None
+        return {"bytes": int(st.bytes), "device_ms": float(st.device_ms),
+                "direction": "download" if st.direction == 1 else "upload", "payload": self.payload}
 
 
 class Decoder:
