@@ -60,6 +60,17 @@ enum {
   RSTR_ROLE_GATE = 12, RSTR_ROLE_UP = 13, RSTR_ROLE_DOWN = 14
 };
 
+/* One host tensor as stored in a checkpoint: dtype 0 = f32, 1 = f16, 2 = bf16
+ * (the SafeTensors "F32"/"F16"/"BF16" of safetensors.clj:48-72), little-endian,
+ * linear weights row-major [out][in]. */
+typedef struct rstr_tensor_raw {
+  int32_t layer;   /* -1 for global tensors (embed, final norm) */
+  int32_t role;
+  int32_t dtype;
+  const void* data;
+  int64_t elements;
+} rstr_tensor_raw;
+
 /* One host f32 tensor: linear weights row-major [out][in] (decoder.clj:77-86). */
 typedef struct rstr_tensor {
   int32_t layer;   /* -1 for global tensors (embed, final norm) */
@@ -90,6 +101,14 @@ int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, const rstr_ten
  * offset, or 1+N(0,0.02)). */
 int rstr_model_bind_synthetic(rstr_session* s, const rstr_model_desc* desc, uint64_t seed,
                               rstr_model** out);
+/* Replaces load-hf's read-tensor-floats + quantize-stream (decoder.clj:31-56,
+ * 152-189; safetensors.clj:48-152) for checkpoint tensors left in their stored
+ * dtype (e.g. pointers into a memory-mapped .safetensors file): each tensor is
+ * copied to the device as stored, widened to f32 there (exactly) and quantised
+ * by the same device packer as rstr_model_bind, so binding from bf16 equals
+ * binding the f32 widening of the same tensors. */
+int rstr_model_bind_raw(rstr_session* s, const rstr_model_desc* desc, const rstr_tensor_raw* tensors,
+                        int32_t n_tensors, rstr_model** out);
 int rstr_model_close(rstr_model* m);
 /* Device bytes of the packed linear weights streamed by one decode step. */
 int64_t rstr_model_weight_bytes(const rstr_model* m);

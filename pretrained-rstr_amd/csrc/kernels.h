@@ -115,6 +115,8 @@ hipError_t launch_append_rows(hipStream_t st, const float* k_rows, const float* 
                               int kvr, const int32_t* slots, uint16_t* kpages, uint16_t* vpages);
 hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64_t page_elems,
                              const int32_t* pairs, int npairs);
+// dtype 0: f32, 1: f16, 2: bf16 -> f32 (exact)
+hipError_t launch_widen(hipStream_t st, int dtype, const void* src, float* dst, int64_t n);
 // mode 0: pool -> fp16 payload; 1: fp16 payload -> pool; 2: f32 payload -> pool (RNE)
 hipError_t launch_chunk_move(hipStream_t st, int mode, uint16_t** slabs, int nslabs, const int32_t* pages,
                              int start, int count, int page_size, int ept, void* payload);

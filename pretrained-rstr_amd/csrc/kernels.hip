@@ -1773,6 +1773,23 @@ hipError_t launch_copy_pages(hipStream_t st, uint16_t** slabs, int nslabs, int64
   return hipGetLastError();
 }
 
+// Checkpoint tensors to f32 on the device (safetensors.clj:48-72 read-tensor-
+// floats): F16 widens exactly, BF16 is the upper half of an f32 bit pattern.
+__global__ void k_widen(int dtype, const void* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (dtype == 1) dst[i] = (float)static_cast<const _Float16*>(src)[i];
+  else if (dtype == 2) dst[i] = __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(src)[i] << 16);
+  else dst[i] = static_cast<const float*>(src)[i];
+}
+
+hipError_t launch_widen(hipStream_t st, int dtype, const void* src, float* dst, int64_t n) {
+  if (n <= 0) return hipSuccess;
+  if (dtype < 0 || dtype > 2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_widen, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dtype, src, dst, n);
+  return hipGetLastError();
+}
+
 // Durable chunk transfer: token rows between the page pool and a dense payload
 // in the portable layout (page_pool.clj:1111-1374; payload order of
 // attention_state.clj:103-123: slab K then V, layer, token; a row is `ept`

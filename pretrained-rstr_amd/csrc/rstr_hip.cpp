@@ -398,8 +398,10 @@ extern "C" int rstr_model_bind_synthetic(rstr_session* s, const rstr_model_desc*
   return RSTR_OK;
 }
 
-extern "C" int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, const rstr_tensor* tensors,
-                               int32_t n_tensors, rstr_model** out) {
+// Bind host tensors of f32 (0), f16 (1) or bf16 (2) elements: each is uploaded
+// as stored, widened to f32 on the device and quantised there.
+static int bind_tensors(rstr_session* s, const rstr_model_desc* desc, int32_t n_tensors,
+                        const rstr_tensor_raw* tensors, rstr_model** out) {
   rstr_model* m = nullptr;
   int rc = model_begin(s, desc, out, &m);
   if (rc) return rc;
@@ -408,34 +410,54 @@ extern "C" int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, con
   // every tensor the flags require must be present exactly once
   std::vector<char> seen((size_t)(d.n_layers + 1) * 16, 0);
   float* tmp = nullptr;
-  size_t tmp_cap = 0;
+  void* raw = nullptr;
+  size_t tmp_cap = 0, raw_cap = 0;
   auto bail = [&](int code, const std::string& msg) {
     if (tmp) hipFree(tmp);
+    if (raw) hipFree(raw);
     model_free(m);
     return fail(s, code, msg);
   };
   for (int32_t i = 0; i < n_tensors; i++) {
-    const rstr_tensor& t = tensors[i];
+    const rstr_tensor_raw& t = tensors[i];
     if (!t.data) return bail(RSTR_E_INVALID, "tensor without data");
+    if (t.dtype < 0 || t.dtype > 2) return bail(RSTR_E_INVALID, "Unsupported dtype");
     int li = t.layer + 1;
     if (li < 0 || li > d.n_layers || t.role < 0 || t.role > 14)
       return bail(RSTR_E_INVALID, "tensor layer or role out of range");
     if (seen[(size_t)li * 16 + t.role]) return bail(RSTR_E_INVALID, "duplicate tensor");
     seen[(size_t)li * 16 + t.role] = 1;
     QTensor* q; int off, n, k;
-    if (linear_slot(m, t.layer, t.role, &q, &off, &n, &k)) {
-      if (t.elements != (int64_t)n * k) return bail(RSTR_E_INVALID, "linear tensor size mismatch");
-      size_t need = (size_t)n * k;
-      if (need > tmp_cap) {
-        if (tmp) hipFree(tmp);
-        tmp = nullptr;
-        if (hipMalloc(&tmp, need * sizeof(float)) != hipSuccess) return bail(RSTR_E_OOM, "hipMalloc");
-        tmp_cap = need;
-      }
-      if (hipMemcpy(tmp, t.data, need * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+    const bool linear = linear_slot(m, t.layer, t.role, &q, &off, &n, &k) != 0;
+    int n2 = 0;
+    float* g = linear ? nullptr : norm_slot(m, t.layer, t.role, &n2);
+    if (!linear && !g) return bail(RSTR_E_INVALID, "tensor role not used by this descriptor");
+    const size_t need = linear ? (size_t)n * k : (size_t)n2;
+    if ((size_t)t.elements != need)
+      return bail(RSTR_E_INVALID, linear ? "linear tensor size mismatch" : "norm tensor size mismatch");
+    const size_t esz = t.dtype == 0 ? 4 : 2;
+    if (need > tmp_cap) {
+      if (tmp) hipFree(tmp);
+      tmp = nullptr;
+      if (hipMalloc(&tmp, need * sizeof(float)) != hipSuccess) return bail(RSTR_E_OOM, "hipMalloc");
+      tmp_cap = need;
+    }
+    if (t.dtype == 0) {
+      if (hipMemcpy(tmp, t.data, need * 4, hipMemcpyHostToDevice) != hipSuccess)
         return bail(RSTR_E_HIP, "weight upload failed");
-      if (launch_gen_linear(st, *q, off, n, k, 0, tmp) != hipSuccess ||
-          hipStreamSynchronize(st) != hipSuccess)
+    } else {
+      if (need * esz > raw_cap) {
+        if (raw) hipFree(raw);
+        raw = nullptr;
+        if (hipMalloc(&raw, need * esz) != hipSuccess) return bail(RSTR_E_OOM, "hipMalloc");
+        raw_cap = need * esz;
+      }
+      if (hipMemcpy(raw, t.data, need * esz, hipMemcpyHostToDevice) != hipSuccess ||
+          launch_widen(st, t.dtype, raw, tmp, (int64_t)need) != hipSuccess)
+        return bail(RSTR_E_HIP, "weight upload failed");
+    }
+    if (linear) {
+      if (launch_gen_linear(st, *q, off, n, k, 0, tmp) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
         return bail(RSTR_E_HIP, "weight quantisation failed");
       if (t.role == RSTR_ROLE_EMBED) {
         double scale = d.embed_scale_sqrt_d ? std::sqrt((double)d.d_model) : 1.0;
@@ -443,17 +465,15 @@ extern "C" int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, con
             hipStreamSynchronize(st) != hipSuccess)
           return bail(RSTR_E_HIP, "embedding prescale failed");
       }
-      continue;
-    }
-    int n2;
-    float* g = norm_slot(m, t.layer, t.role, &n2);
-    if (!g) return bail(RSTR_E_INVALID, "tensor role not used by this descriptor");
-    if (t.elements != n2) return bail(RSTR_E_INVALID, "norm tensor size mismatch");
-    if (hipMemcpy(g, t.data, sizeof(float) * n2, hipMemcpyHostToDevice) != hipSuccess)
+    } else if (hipMemcpyAsync(g, tmp, sizeof(float) * n2, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+               hipStreamSynchronize(st) != hipSuccess) {
       return bail(RSTR_E_HIP, "norm upload failed");
+    }
   }
   if (tmp) hipFree(tmp);
+  if (raw) hipFree(raw);
   tmp = nullptr;
+  raw = nullptr;
   auto need = [&](int layer, int role) { return seen[(size_t)(layer + 1) * 16 + role] != 0; };
   bool ok = need(-1, RSTR_ROLE_EMBED) && need(-1, RSTR_ROLE_FINAL_NORM);
   for (int l = 0; l < d.n_layers && ok; l++) {
@@ -468,6 +488,21 @@ extern "C" int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, con
   }
   *out = m;
   return RSTR_OK;
+}
+
+extern "C" int rstr_model_bind(rstr_session* s, const rstr_model_desc* desc, const rstr_tensor* tensors,
+                               int32_t n_tensors, rstr_model** out) {
+  if (n_tensors < 0 || (n_tensors && !tensors)) return fail(s, RSTR_E_INVALID, "invalid tensor list");
+  std::vector<rstr_tensor_raw> raw((size_t)n_tensors);
+  for (int32_t i = 0; i < n_tensors; i++)
+    raw[i] = rstr_tensor_raw{tensors[i].layer, tensors[i].role, 0, tensors[i].data, tensors[i].elements};
+  return bind_tensors(s, desc, n_tensors, raw.data(), out);
+}
+
+extern "C" int rstr_model_bind_raw(rstr_session* s, const rstr_model_desc* desc, const rstr_tensor_raw* tensors,
+                                   int32_t n_tensors, rstr_model** out) {
+  if (n_tensors < 0 || (n_tensors && !tensors)) return fail(s, RSTR_E_INVALID, "invalid tensor list");
+  return bind_tensors(s, desc, n_tensors, tensors, out);
 }
 
 extern "C" int rstr_model_close(rstr_model* m) {

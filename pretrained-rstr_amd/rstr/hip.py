@@ -23,7 +23,7 @@ KERNEL_CLASSES = ("qgemm", "head", "attn_split", "attn_merge", "qkv_post", "rows
 EXPORTS = (
     "rstr_session_open", "rstr_session_close", "rstr_last_error", "rstr_open_error",
     "rstr_session_memory",
-    "rstr_model_bind", "rstr_model_bind_synthetic", "rstr_model_close", "rstr_model_weight_bytes",
+    "rstr_model_bind", "rstr_model_bind_raw", "rstr_model_bind_synthetic", "rstr_model_close", "rstr_model_weight_bytes",
     "rstr_model_export_linear", "rstr_pool_open", "rstr_pool_close", "rstr_pool_copy_page",
     "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_chunk_export_submit",
     "rstr_chunk_restore_submit", "rstr_transfer_done", "rstr_transfer_complete", "rstr_chunk_bench", "rstr_decoder_open",
@@ -54,6 +54,14 @@ class Desc(C.Structure):
 class Tensor(C.Structure):
     _fields_ = [("layer", C.c_int32), ("role", C.c_int32), ("data", C.c_void_p),
                 ("elements", C.c_int64)]
+
+
+class RawTensor(C.Structure):
+    _fields_ = [("layer", C.c_int32), ("role", C.c_int32), ("dtype", C.c_int32), ("data", C.c_void_p),
+                ("elements", C.c_int64)]
+
+
+RAW_DTYPES = {"F32": 0, "F16": 1, "BF16": 2}
 
 
 class TransferStats(C.Structure):
@@ -88,6 +96,7 @@ def lib():
             "rstr_session_memory": (i32, [P, C.POINTER(i64), C.POINTER(i64)]),
             "rstr_model_bind": (i32, [P, P, P, i32, C.POINTER(P)]),
             "rstr_model_bind_synthetic": (i32, [P, P, u64, C.POINTER(P)]),
+            "rstr_model_bind_raw": (i32, [P, P, P, i32, C.POINTER(P)]),
             "rstr_model_close": (i32, [P]),
             "rstr_model_weight_bytes": (i64, [P]),
             "rstr_model_export_linear": (i32, [P, i32, i32, P, P]),
@@ -190,11 +199,27 @@ class Session:
 class Model:
     """Resident quantised model (decoder-gpu/bind-decode! weights)."""
 
-    def __init__(self, sess: Session, cfg: dict, seed: int | None = None, tensors=None):
+    def __init__(self, sess: Session, cfg: dict, seed: int | None = None, tensors=None, raw_tensors=None):
+        """``tensors``: (layer, role, f32 array); ``raw_tensors``: (layer, role,
+        "F32" | "F16" | "BF16", array of the stored elements -- float32, float16
+        or the bf16 bit patterns as uint16), e.g. views of a mapped checkpoint."""
         self.sess, self.cfg = sess, dict(cfg)
         self._desc = make_desc(cfg)
         h = C.c_void_p()
-        if tensors is None:
+        if raw_tensors is not None:
+            keep = []
+            arr = (RawTensor * len(raw_tensors))()
+            for i, (layer, role, dtype, data) in enumerate(raw_tensors):
+                code = RAW_DTYPES[dtype]
+                data = np.ascontiguousarray(data).reshape(-1)
+                if data.itemsize != (4 if code == 0 else 2):
+                    raise ValueError(f"{dtype} tensor with {data.dtype} elements")
+                keep.append(data)
+                arr[i] = RawTensor(layer, ROLE[role] if isinstance(role, str) else role, code,
+                                   data.ctypes.data, data.size)
+            rc = lib().rstr_model_bind_raw(sess.h, C.byref(self._desc), C.cast(arr, C.c_void_p),
+                                           len(raw_tensors), C.byref(h))
+        elif tensors is None:
             rc = lib().rstr_model_bind_synthetic(sess.h, C.byref(self._desc), int(seed), C.byref(h))
         else:
             keep = []
