@@ -156,3 +156,37 @@ def test_device_rejects_bad_ranges_and_dtypes():
         assert st["bytes"] == p.chunk_elements(2) * 2 and st["direction"] == "upload"
         with pytest.raises(hip.RstrError, match="already completed"):
             t.complete()
+
+
+def test_restored_prefix_continues_exactly_like_the_original_route():
+    """Export a route's first 48 tokens (computed through bulk prefill tiles),
+    restore them into a fresh route, and generate from the same prompt: only the
+    uncached suffix is computed (paged_decoder.clj:774-813) and the tokens equal
+    the original route's."""
+    print("case chunk restore then decode", flush=True)
+    from rstr.paged_decoder import HipStepDevice, PagedDecoder
+    ps, P, maxpos, T = 16, 40, 128, 24
+    pps = maxpos // ps
+    prompt = [int(x) for x in np.random.default_rng(4).integers(0, CFG["vocab"], 61)]
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=6)
+        p = hip.Pool(m, ps, P)
+        d = hip.Decoder(m, p, 1, pps, maxpos, 16)
+        pf = hip.Prefill(m, p, T, pps, maxpos, 16)
+        pool = _mirror(p, ps, P, CFG)
+        dev = HipStepDevice(d, pf)
+        dec = PagedDecoder(pool, dev, batch_size=1, maxpos=maxpos, pages_per_sequence=pps, prefill_T=T)
+        want = dec.generate("a", prompt, 6)
+        chunk = chunks.export_chunk(pool, "a", "fp", {"chunk/start": 0, "chunk/token-count": 48})
+        pool.allocate_route("b", 48)
+        chunks.restore_chunk(pool, "b", _desc(pool, 0, 48), chunk["chunk/payload"])
+        ran = []
+        orig = dev.run_prefill
+        dev.run_prefill = lambda: (ran.append(1), orig())
+        got = dec.generate("b", prompt, 6)
+        assert got == want
+        assert ran == []  # the restored 48 tokens are not recomputed; 12 suffix tokens decode singly
+        # the restored route's pages hold the same K/V as the original's over the prefix
+        ra, rb = pool.route("a"), pool.route("b")
+        slabs = _slabs(p, CFG["n_layers"])
+        assert np.array_equal(OC.gather(slabs, ra.pages, ps, 0, 60), OC.gather(slabs, rb.pages, ps, 0, 60))

@@ -18,11 +18,14 @@ from rstr import configs, hip
 from rstr.page_pool import PagePool
 from rstr.paged_decoder import PagedDecoder, HipStepDevice, DESCRIPTOR_KEYS
 
-CFG = configs.MODELS["tiny_llama"]
+MODELS = ["tiny_llama", "tiny_gemma", "tiny_qwen"]   # plain, windowed + sandwich + dual RoPE, qk-norm
 PS, PAGES, MAXPOS, SPLIT, SEED, T = 16, 40, 160, 32, 9, 24
 PPS = MAXPOS // PS
-PROMPT = [int(x) for x in np.random.default_rng(3).integers(0, CFG["vocab"], 61)]
 MAX_NEW = 5
+
+
+def _prompt(cfg):
+    return [int(x) for x in np.random.default_rng(3).integers(0, cfg["vocab"], 61)]
 
 
 def prefill_lane_descriptors(desc: dict, batch: int) -> dict:
@@ -97,19 +100,19 @@ class OracleDevice:
         self.tiles += 1
 
 
-def _generate(device, batch_of_pool_device, prefill_T):
-    pool = PagePool(PS, PAGES, CFG["n_layers"], CFG["n_kv"], CFG["head_dim"], device=batch_of_pool_device)
+def _generate(cfg, device, batch_of_pool_device, prefill_T):
+    pool = PagePool(PS, PAGES, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"], device=batch_of_pool_device)
     dec = PagedDecoder(pool, device, batch_size=1, maxpos=MAXPOS, pages_per_sequence=PPS, prefill_T=prefill_T)
-    toks = dec.generate("c", PROMPT, MAX_NEW)
+    toks = dec.generate("c", _prompt(cfg), MAX_NEW)
     return toks, pool.route("c").pages
 
 
-def _oracle_token_by_token():
-    om = O.Model(CFG, seed=SEED)
+def _oracle_token_by_token(cfg):
+    om = O.Model(cfg, seed=SEED)
     od = O.Decoder(om, 1, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=SPLIT)
     try:
-        toks, pages = _generate(OracleDevice(od), od, None)
-        slabs = [(od.slab(s, l).view(np.uint16).copy()) for l in range(CFG["n_layers"]) for s in (0, 1)]
+        toks, pages = _generate(cfg, OracleDevice(od), od, None)
+        slabs = [(od.slab(s, l).view(np.uint16).copy()) for l in range(cfg["n_layers"]) for s in (0, 1)]
         return toks, pages, slabs
     finally:
         od.close()
@@ -126,17 +129,19 @@ def test_prefill_lane_descriptors_are_causal_rows_of_one_route():
     assert d["row_offsets"].tolist() == [0, 1, 2, 3, 4]
 
 
-def test_oracle_prefill_tiles_equal_token_by_token_priming():
-    want_toks, want_pages, want_slabs = _oracle_token_by_token()
-    om = O.Model(CFG, seed=SEED)
+@pytest.mark.parametrize("name", MODELS)
+def test_oracle_prefill_tiles_equal_token_by_token_priming(name):
+    cfg = configs.MODELS[name]
+    want_toks, want_pages, want_slabs = _oracle_token_by_token(cfg)
+    om = O.Model(cfg, seed=SEED)
     od = O.Decoder(om, T, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=SPLIT)
     try:
         dev = OracleDevice(od)
-        toks, pages = _generate(dev, od, T)
-        assert dev.tiles == (len(PROMPT) - 1) // T == 2
+        toks, pages = _generate(cfg, dev, od, T)
+        assert dev.tiles == (len(_prompt(cfg)) - 1) // T == 2
         assert toks == want_toks
         assert pages == want_pages
-        for i, (l, s) in enumerate((l, s) for l in range(CFG["n_layers"]) for s in (0, 1)):
+        for i, (l, s) in enumerate((l, s) for l in range(cfg["n_layers"]) for s in (0, 1)):
             assert np.array_equal(od.slab(s, l).view(np.uint16), want_slabs[i]), (l, s)
     finally:
         od.close()
@@ -144,28 +149,31 @@ def test_oracle_prefill_tiles_equal_token_by_token_priming():
 
 
 @pytest.mark.gpu
-def test_gpu_prefill_tiles_equal_oracle_token_by_token():
-    print("case prefill tiles", flush=True)
-    want_toks, want_pages, want_slabs = _oracle_token_by_token()
+@pytest.mark.parametrize("name", MODELS)
+def test_gpu_prefill_tiles_equal_oracle_token_by_token(name):
+    print("case prefill tiles", name, flush=True)
+    cfg = configs.MODELS[name]
+    want_toks, want_pages, want_slabs = _oracle_token_by_token(cfg)
     with hip.Session(0) as sess:
-        m = hip.Model(sess, CFG, seed=SEED)
+        m = hip.Model(sess, cfg, seed=SEED)
         p = hip.Pool(m, PS, PAGES)
         d1 = hip.Decoder(m, p, 1, PPS, MAXPOS, SPLIT)
         pf = hip.Prefill(m, p, T, PPS, MAXPOS, SPLIT)
         dev = HipStepDevice(d1, pf)
-        toks, pages = _generate(dev, p, T)
+        toks, pages = _generate(cfg, dev, p, T)
         assert dev._prefill is not None
         assert toks == want_toks
         assert pages == want_pages
-        for i, (l, s) in enumerate((l, s) for l in range(CFG["n_layers"]) for s in (0, 1)):
+        for i, (l, s) in enumerate((l, s) for l in range(cfg["n_layers"]) for s in (0, 1)):
             assert np.array_equal(p.pages(s, l).view(np.uint16).ravel(), want_slabs[i].ravel()), (l, s)
 
 
 @pytest.mark.gpu
 def test_gpu_prefill_decoder_rejects_decode_calls_and_bad_tiles():
     print("case prefill errors", flush=True)
+    cfg = configs.MODELS["tiny_llama"]
     with hip.Session(0) as sess:
-        m = hip.Model(sess, CFG, seed=SEED)
+        m = hip.Model(sess, cfg, seed=SEED)
         p = hip.Pool(m, PS, PAGES)
         pf = hip.Prefill(m, p, 4, PPS, MAXPOS, SPLIT)
         z = np.zeros(4, np.int32)
