@@ -71,10 +71,13 @@ class ModelWorker:
 def open_worker(model_directory: str, fingerprint: str, worker_id=":worker-a", device: int = 0,
                 max_position: int = 1024, page_size: int = 16, physical_pages: int | None = None,
                 chunk_size: int = 16, eos_ids=None, measurements=None, prefill_T: int | None = None,
-                split: int = 256, weight_bits: int | None = None) -> ModelWorker:
+                split: int = 64, weight_bits: int | None = None) -> ModelWorker:
     """model_worker.clj:52-130 for the decode path: validates the options, binds
     the checkpoint and opens pool and decoder; anything opened is closed again
-    if a later step fails."""
+    if a later step fails.  ``split`` is the attention history tile (it fixes
+    the attention's reduction order); a one-lane decoder has few work items, and
+    64-token tiles made a Llama-3-8B-shaped step at 512 tokens of context 17%
+    shorter than 256-token ones (2.82 vs 3.38 ms)."""
     if not isinstance(fingerprint, str):
         raise WorkerError("Model worker requires a compatibility fingerprint")
     max_position, page_size = int(max_position), int(page_size)
