@@ -59,3 +59,19 @@ def test_config3_shape_schedule_matches_oracle():
     pl = workload.SharedPrefixPlanner(cfg, batch, 16, pages, maxpos, seed=2)
     _replay(cfg, pl, batch, pages, maxpos, 128, 2)
     assert pl.cow_pages > 0
+
+
+def test_config5_shape_one_step_matches_oracle():
+    """The north-star shape (Llama-3-8B Q4, all 32 layers and the 128 256-token
+    head) at 128 ragged lanes: the first two planned steps (admission fills, primes,
+    one decode step each) give the oracle's tokens in every lane.  Prompts are
+    drawn from U[128, 1024] instead of the bench's U[128, 4096] to bound the
+    oracle's host KV memory."""
+    print("case config5 shape", flush=True)
+    cfg = configs.LLAMA3_8B
+    batch, maxpos = 128, 1024 + 64
+    pages = 128 * (maxpos // 16 + 1)
+    pl = workload.ChurnPlanner(cfg, batch, 16, pages, maxpos, seed=5, arrival_mean=4.0,
+                               prompt=(128, 1024), output=(32, 64))
+    steps = _replay(cfg, pl, batch, pages, maxpos, 256, 2)
+    assert all(st["active"] == batch for st in steps)
