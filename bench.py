@@ -43,7 +43,7 @@ WORKLOADS = {
 }
 
 
-# isolated attention workloads (SURVEY 8(d) config 4): (model shape, lanes, seed)
+# isolated attention workloads (BASELINE.json configs[3]): (model shape, lanes, seed)
 ATTN_WORKLOADS = {"config4": ("llama3_8b", 128, 4)}
 
 

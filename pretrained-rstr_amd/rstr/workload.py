@@ -164,7 +164,7 @@ class ChurnPlanner:
 
 class SharedPrefixPlanner:
     """A fixed set of decode lanes whose first ``shared_lanes`` fork one resident
-    prefix (SURVEY 8(d) config 3): contexts log-uniform in ``ctx``; a lane of
+    prefix (BASELINE.json configs[2]): contexts log-uniform in ``ctx``; a lane of
     the shared group forks the prefix route at min(ctx, prefix) - 1 rows
     (``fork-route!``, page_pool.clj:679-724) and appends its private rows with a
     range reservation, so the shared partial tail page is copied on the first

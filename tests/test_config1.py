@@ -1,4 +1,4 @@
-"""BASELINE configs[0] as a parity case: the Gemma-3-270M-shaped decoder with Q8
+"""BASELINE.json configs[0] as a parity case: the Gemma-3-270M-shaped decoder with Q8
 weights (all 18 layers, 262 144-token vocabulary, sliding window 512), one lane,
 a 32-token prompt of uniform ids (seed 0) and 64 greedy steps, generated through
 the paged-decoder mirror on the HIP decoder and on the CPU oracle: the same 64

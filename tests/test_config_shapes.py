@@ -1,4 +1,4 @@
-"""BASELINE configs[1] and configs[2] at their real shapes as parity cases: the
+"""BASELINE.json configs[1], [2] and [4] at their real shapes as parity cases: the
 bench's host-planned schedules replayed on the HIP decoder (fills, copy-on-write
 copies, primes, one step graph per step) and on the oracle, token for token.
 
@@ -6,7 +6,9 @@ copies, primes, one step graph per step) and on the oracle, token for token.
   contexts U[64, 2048] admitted onto a permuted page pool (attention split 64).
 - config3: Qwen3-0.6B-shaped Q4 (28 layers, qk-norm), 64 lanes, contexts
   log-uniform [256, 8192], lanes 0-31 forking one 1024-token prefix with
-  copy-on-write on their first divergent append (attention split 128)."""
+  copy-on-write on their first divergent append (attention split 128).
+- config5: Llama-3-8B-shaped Q4 (32 layers), 128 lanes with churn (prompts capped
+  at 1024 tokens to bound the oracle's host KV memory)."""
 import numpy as np
 import pytest
 
