@@ -192,3 +192,40 @@ def test_gpu_prefill_decoder_rejects_decode_calls_and_bad_tiles():
         pf.prefill_range([1, 2, 3, 4], [48, 49, 50, 51], [0, 1, 2, 3], row, 4, 0)
         with pytest.raises(hip.RstrError, match="schedules"):
             sess.check(hip.lib().rstr_schedule_upload(pf.h, None, 1))
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_wide_tiles_at_llama_width_equal_the_oracle():
+    """Llama-3-8B width (d 4096, 32/8 heads, hd 128, vocab 128 256; first layer
+    only): a 600-token prompt in two 256-row tiles plus an 87-token scalar tail
+    writes the same K/V as the oracle primed token by token, and the next
+    tokens agree."""
+    print("case prefill llama width", flush=True)
+    cfg = dict(configs.MODELS["llama3_8b"], n_layers=1)
+    ps, maxpos, split, tile = 16, 640, 256, 256
+    pps, pages = maxpos // ps, maxpos // ps + 2
+    prompt = [int(x) for x in np.random.default_rng(8).integers(0, cfg["vocab"], 600)]
+
+    def gen(device, pool_device, prefill_T):
+        pool = PagePool(ps, pages, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"], device=pool_device)
+        dec = PagedDecoder(pool, device, batch_size=1, maxpos=maxpos, pages_per_sequence=pps, prefill_T=prefill_T)
+        return dec.generate("c", prompt, 3), pool.route("c").pages
+
+    om = O.Model(cfg, seed=SEED)
+    od = O.Decoder(om, 1, ps, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        want, want_pages = gen(OracleDevice(od), od, None)
+        want_slabs = [od.slab(s, 0).view(np.uint16).copy() for s in (0, 1)]
+    finally:
+        od.close()
+        om.close()
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, cfg, seed=SEED)
+        p = hip.Pool(m, ps, pages)
+        d1 = hip.Decoder(m, p, 1, pps, maxpos, split)
+        pf = hip.Prefill(m, p, tile, pps, maxpos, split)
+        got, pages_got = gen(HipStepDevice(d1, pf), p, tile)
+        got_slabs = [p.pages(s, 0).view(np.uint16).ravel() for s in (0, 1)]
+    assert got == want and pages_got == want_pages
+    for a, b in zip(got_slabs, want_slabs):
+        assert np.array_equal(a, b.ravel())
