@@ -445,15 +445,19 @@ struct QgPlan {
 };
 // Tile plan from the padded batch (row tiles) and the requested number of K
 // slices (4/nq).  Measured on MI355X at the decode shapes (N 4096..128256,
-// K 4096/14336): 64-row x 16-column wave tiles for batches above 48 rows,
-// 32 x 32 for 17..48 rows; up to 16 rows, 16 x 16 per quarter (one K quarter
-// per wave: the most waves streaming weights, 20-28% faster than 16 x 32 at
-// 1 and 16 rows), 16 x 64 for one-slice heads.
+// K 4096/14336): 64-row x 16-column wave tiles for batches above 64 rows and
+// for 49..64 rows with two or one K slices, 32 x 16 for 49..64 rows with four
+// K slices (twice the workgroups; 15-20% faster on the four-slice QKV, O and
+// down at 64 rows, equal or slower at 128), 32 x 32 for 17..48 rows; up to 16
+// rows, 16 x 16 per quarter (one K quarter per wave: the most waves streaming
+// weights, 20-28% faster than 16 x 32 at 1 and 16 rows), 16 x 64 for
+// one-slice heads.
 QgPlan qg_plan(int mpad, int splits, int bits) {
   const int mt_all = mpad / 16;
   QgPlan p{};
   p.nq = 4 / splits;
-  if (mt_all > 3) { p.rt = 4; p.ct = 1; }
+  if (mt_all == 4 && p.nq == 1) { p.rt = 2; p.ct = 1; }
+  else if (mt_all > 3) { p.rt = 4; p.ct = 1; }
   else if (mt_all > 1) { p.rt = 2; p.ct = 2; }
   else { p.rt = 1; p.ct = p.nq == 1 ? 1 : (p.nq == 4 && bits == 4) ? 4 : 2; }
   return p;
@@ -499,6 +503,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 #define RSTR_QG_T(B)                                   \
   do {                                                 \
     if (p.rt == 4) RSTR_QG_Q(4, 1, B);                 \
+    else if (p.rt == 2 && p.ct == 1) RSTR_QG(2, 1, B, 1); \
     else if (p.rt == 2) RSTR_QG_Q(2, 2, B);            \
     else if (p.ct == 4) RSTR_QG_Q(1, 4, B);            \
     else if (p.ct == 2) RSTR_QG_Q(1, 2, B);            \

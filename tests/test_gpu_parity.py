@@ -380,10 +380,11 @@ def test_lane_results_do_not_depend_on_the_batch(sess):
         _close(one)
 
 
-@pytest.mark.parametrize("B", [40, 100, 130])
+@pytest.mark.parametrize("B", [40, 60, 100, 130])
 def test_wide_batches_bit_exact(sess, B):
-    """Row-tile groupings of the projection kernel (1, 2 and 3 row groups of up to
-    128 rows; split-K slices) against the oracle."""
+    """Row-tile groupings of the projection kernel (32 x 32 wave tiles at 40 rows,
+    32 x 16 at 60, 64 x 16 in 2 and 3 row groups at 100 and 130; split-K slices)
+    against the oracle."""
     print(f"case wide batch B={B}", flush=True)
     cfg = configs.TINY_QWEN
     rng = np.random.default_rng(B)
