@@ -1570,34 +1570,59 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
 #pragma unroll
   for (int d = 0; d < DPL; d++) O[d] = 0.0f;
   if (len > 0 && ns > 0) {
+    // Split partials, in split order; every load of a round is issued before
+    // its first use.  Round 0: the o of splits 0..15 with the m and l of split
+    // `lane` (and the m of splits lane+64, ... for the maximum); then 16 splits'
+    // o per round.  w_k = exp(m_k - M) is computed once by lane k mod 64 and
+    // read from that lane (same value, same order of the fmas below).
+    constexpr int C = 16;
     const int stride = G * (HD + 2);
-    float M = -__builtin_inff();
-    for (int kk = lane; kk < ns; kk += 64)
-      M = fmaxf(M, part[(size_t)(base + kk) * stride + hl * (HD + 2) + HD]);
+    const float* pb = part + (size_t)base * stride + hl * (HD + 2);
+    float ok[C][DPL];
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const float* pr = pb + (size_t)min(j, ns - 1) * stride;
+#pragma unroll
+      for (int d = 0; d < DPL; d++) ok[j][d] = pr[lane * DPL + d];
+    }
+    const float* p0 = pb + (size_t)min(lane, ns - 1) * stride;
+    const float m0 = p0[HD], l0 = p0[HD + 1];
+    float M = m0;
+    for (int kk = lane + 64; kk < ns; kk += 64) M = fmaxf(M, pb[(size_t)kk * stride + HD]);
     M = wave_max(M);
     float L = 0.0f;
-    // splits in order, their partials loaded 8 at a time
-    for (int k0 = 0; k0 < ns; k0 += 8) {
-      float mk[8], lk[8], ok[8][DPL];
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float* pr = part + (size_t)(base + min(k0 + j, ns - 1)) * stride + hl * (HD + 2);
-        mk[j] = pr[HD];
-        lk[j] = pr[HD + 1];
-#pragma unroll
-        for (int d = 0; d < DPL; d++) ok[j][d] = pr[lane * DPL + d];
+    for (int g0 = 0; g0 < ns; g0 += 64) {
+      float wl, ll;
+      if (g0 == 0) {
+        wl = dexp(m0 - M);
+        ll = l0;
+      } else {
+        const float* pk = pb + (size_t)min(g0 + lane, ns - 1) * stride;
+        wl = dexp(pk[HD] - M);
+        ll = pk[HD + 1];
       }
+      const int gn = min(64, ns - g0);
+      for (int c0 = 0; c0 < gn; c0 += C) {
+        if (g0 + c0 > 0) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        if (k0 + j < ns) {
-          const float w = dexp(mk[j] - M);
-          L = __builtin_fmaf(lk[j], w, L);
+          for (int j = 0; j < C; j++) {
+            const float* pr = pb + (size_t)min(g0 + c0 + j, ns - 1) * stride;
 #pragma unroll
-          for (int d = 0; d < DPL; d++) O[d] = __builtin_fmaf(ok[j][d], w, O[d]);
+            for (int d = 0; d < DPL; d++) ok[j][d] = pr[lane * DPL + d];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+          if (c0 + j < gn) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), c0 + j));
+            const float lk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ll), c0 + j));
+            L = __builtin_fmaf(lk, w, L);
+#pragma unroll
+            for (int d = 0; d < DPL; d++) O[d] = __builtin_fmaf(ok[j][d], w, O[d]);
+          }
         }
       }
     }
-#pragma unroll
     for (int d = 0; d < DPL; d++) O[d] = O[d] / L;
   }
   if (out_f32) {

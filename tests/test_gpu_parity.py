@@ -200,6 +200,43 @@ def test_append_rejects_duplicate_slots(sess):
 # ---------------------------------------------------------------------------
 # attention vs the oracle on random ragged inputs
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 8, 2), (64, 4, 4)])
+@pytest.mark.parametrize("split,window", [(16, 0), (32, 700)])
+def test_attention_many_splits_matches_oracle(sess, hd, n_q, n_kv, split, window):
+    """Routes of up to 69 splits: the merge's rounds of 16 splits and its second
+    group of 64 (exp weights read from the lane that computed them)."""
+    print(f"case attention many splits hd{hd} q{n_q} kv{n_kv} split{split} window{window}", flush=True)
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
+               head_dim=hd)
+    lengths = np.array([1100, 300, 0, 1025, 17, 257], np.int32)
+    B, ps, pps = len(lengths), 16, 72
+    pages = int(sum(-(-n // ps) for n in lengths)) + 4
+    rng = np.random.default_rng(hd * 7 + split + window)
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        perm = rng.permutation(pages).astype(np.int32)
+        pt = np.full((B, pps), -1, np.int32)
+        used = 0
+        for b in range(B):
+            n = -(-lengths[b] // ps)
+            pt[b, :n] = perm[used:used + n]
+            used += n
+        q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        got = p.attention(0, q, pt, lengths, window=window, scale=scale, split=split)
+        want = O.attention(q, kp, vp, pt, lengths, window, scale, split)
+        assert np.array_equal(got, want)
+        assert np.all(got[2] == 0) and np.isfinite(got).all()
+    finally:
+        p.close()
+        m.close()
+
+
 @pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (256, 4, 1), (64, 8, 2), (128, 16, 8), (128, 4, 1)])
 @pytest.mark.parametrize("split,window", [(256, 0), (32, 0), (16, 24)])
 def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
