@@ -445,18 +445,19 @@ struct QgPlan {
 };
 // Tile plan from the padded batch (row tiles) and the requested number of K
 // slices (4/nq).  Measured on MI355X at the decode shapes (N 4096..128256,
-// K 4096/14336): 64-row x 16-column wave tiles for batches above 64 rows and
-// for 49..64 rows with two or one K slices, 32 x 16 for 49..64 rows with four
-// K slices (twice the workgroups; 15-20% faster on the four-slice QKV, O and
-// down at 64 rows, equal or slower at 128), 32 x 32 for 17..48 rows; up to 16
+// K 4096/14336): 64-row x 16-column wave tiles above 48 rows, except 32 x 16
+// with four K slices at 49..64 rows (twice the workgroups; QKV, O and down
+// 15-20% faster at 64 rows) and at 65..128 rows for outputs up to 4096 wide
+// (O and down 2-5% faster at 128 rows; QKV at 6144 is not), 32 x 32 for
+// 17..48 rows; up to 16
 // rows, 16 x 16 per quarter (one K quarter per wave: the most waves streaming
 // weights, 20-28% faster than 16 x 32 at 1 and 16 rows), 16 x 64 for
 // one-slice heads.
-QgPlan qg_plan(int mpad, int splits, int bits) {
+QgPlan qg_plan(int mpad, int splits, int bits, int n) {
   const int mt_all = mpad / 16;
   QgPlan p{};
   p.nq = 4 / splits;
-  if (mt_all == 4 && p.nq == 1) { p.rt = 2; p.ct = 1; }
+  if (p.nq == 1 && (mt_all == 4 || (mt_all <= 8 && mt_all > 4 && n <= 4096))) { p.rt = 2; p.ct = 1; }
   else if (mt_all > 3) { p.rt = 4; p.ct = 1; }
   else if (mt_all > 1) { p.rt = 2; p.ct = 2; }
   else { p.rt = 1; p.ct = p.nq == 1 ? 1 : (p.nq == 4 && bits == 4) ? 4 : 2; }
@@ -479,7 +480,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   const int nb = w.k / 32;
   if (w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4)) return hipErrorInvalidValue;
   if (w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
-  const QgPlan p = qg_plan(x.mpad, splits, w.bits);
+  const QgPlan p = qg_plan(x.mpad, splits, w.bits, w.n);
   const int nct = w.n / 16;
   const int mt_all = x.mpad / 16;
   const dim3 grid((nct + 4 * p.ct - 1) / (4 * p.ct), splits, (mt_all + p.rt - 1) / p.rt);
