@@ -1571,11 +1571,11 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
 #pragma unroll
   for (int d = 0; d < DPL; d++) O[d] = 0.0f;
   if (len > 0 && ns > 0) {
-    // Split partials, in split order; every load of a round is issued before
-    // its first use.  Round 0: the o of splits 0..15 with the m and l of split
-    // `lane` (and the m of splits lane+64, ... for the maximum); then 16 splits'
-    // o per round.  w_k = exp(m_k - M) is computed once by lane k mod 64 and
-    // read from that lane (same value, same order of the fmas below).
+    // Split partials, in split order; every load of a batch is issued before
+    // its first use.  First batch: the o of splits 0..15 with the m and l of
+    // split `lane` (and the m of splits lane+64, ... for the maximum); then 16
+    // splits' o per batch.  w_k = exp(m_k - M) is computed once by lane k mod 64
+    // and read from that lane (same value, same order of the fmas below).
     constexpr int C = 16;
     const int stride = G * (HD + 2);
     const float* pb = part + (size_t)base * stride + hl * (HD + 2);
