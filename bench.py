@@ -57,25 +57,7 @@ def attention_workload(args) -> dict:
     name, B, seed = ATTN_WORKLOADS[args.workload]
     cfg = dict(configs.MODELS[name], n_layers=1)
     ps, n_kv, hd, n_q = 16, cfg["n_kv"], cfg["head_dim"], cfg["n_q"]
-    rng = np.random.default_rng(seed)
-    lengths = np.clip(np.rint(np.exp(rng.normal(7.0, 1.2, B))), 16, 32768).astype(np.int32)
-    full = lengths // ps
-    npages = -(-lengths // ps)
-    shared_n = np.rint(0.25 * full).astype(np.int64)
-    S = int(shared_n.max())
-    private = int((npages - shared_n).sum())
-    physical = S + private
-    perm = rng.permutation(physical).astype(np.int32)
-    shared_pages, priv_pages = perm[:S], perm[S:]
-    pps = int(npages.max())
-    pt = np.full((B, pps), -1, np.int32)
-    used = 0
-    for b in range(B):
-        k = int(shared_n[b])
-        pt[b, :k] = shared_pages[:k]
-        n_priv = int(npages[b]) - k
-        pt[b, k:npages[b]] = priv_pages[used:used + n_priv]
-        used += n_priv
+    lengths, pt, physical, shared_n, rng = workload.shared_prefix_routes(B, seed, page_size=ps)
     row_bytes = n_kv * hd * 2 * 2  # fp16 K + V of one token
     logical = int(lengths.sum()) * row_bytes
     unique_tokens = int(shared_n.max()) * ps + int((lengths - shared_n * ps).sum())

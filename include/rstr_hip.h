@@ -242,6 +242,15 @@ int rstr_prefill_range(rstr_decoder* d, const int32_t* tokens, const int32_t* sl
 int rstr_append_run(rstr_pool* p, int32_t layer, int32_t batch, const float* k_rows,
                     const float* v_rows, const int32_t* slots);
 
+/* ---- isolated decode tail ------------------------------------------------------
+ * Replaces decode-tail! (decoder_gpu.clj:73-78; KAT
+ * decoder_gpu_composition_test.clj:9-20) with the decode step's own tail
+ * kernel: per row of logits[rows][vocab] the greedy token (ties -> lowest id,
+ * NaN beats every finite value, lowest NaN id), then that token's row of
+ * emb[vocab][d] gathered into rows_out[rows][d]. */
+int rstr_tail_run(rstr_session* s, int32_t rows, int32_t vocab, int32_t d, const float* logits,
+                  const float* emb, int32_t* tokens_out, float* rows_out);
+
 /* ---- isolated routed attention -----------------------------------------------
  * Replaces paged-attention/run! (paged_attention.clj:322-474) with f32 query
  * and output: q[batch][n_q][head_dim], one query row per sequence

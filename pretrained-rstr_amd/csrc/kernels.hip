@@ -882,7 +882,7 @@ hipError_t launch_qkv_post(hipStream_t st, Slices yqkv, int rows, int n_q, int n
 // holds `split` tokens; only a lane's first (window start) and last split can
 // be partial.
 __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int window, int n_kv, int R,
-                                                   const int32_t* __restrict__ lengths,
+                                                   int max_items, const int32_t* __restrict__ lengths,
                                                    int32_t* __restrict__ tab) {
   // tab: lo[B] k0[B] nsplit[B] base[B+1] fbase[B+1] pbase[B+1]; base, fbase
   // and pbase are exclusive prefix sums over lanes of the lane's items, full
@@ -948,6 +948,20 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     carry_a += s_a[1023];
     carry_f += s_f[1023];
     carry_p += s_p[1023];
+    __syncthreads();
+  }
+  // More items than the work list holds (descriptors the host validation
+  // rejects): the step gets no attention work, so every output is 0, instead
+  // of items written past the list.  carry_a is the same in every thread.
+  if (carry_a > max_items) {
+    for (int b = tid; b < batch; b += 1024) {
+      ns[b] = 0;
+      base[b] = 0;
+      fbase[b] = 0;
+      pbase[b] = 0;
+    }
+    carry_a = carry_f = carry_p = 0;
+    for (int i = tid; i < RSTR_NCH; i += 1024) s_h[i] = 0;
     __syncthreads();
   }
   if (tid == 0) {
@@ -1025,7 +1039,7 @@ hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* le
   if (R <= 0) return hipErrorInvalidValue;
   if (g.batch >= (1 << 20) || g.n_kv >= (1 << 11)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(1024), 0, st, g.batch, g.split, g.window, g.n_kv, R,
-                     lengths, lane_tab);
+                     max_items, lengths, lane_tab);
   hipLaunchKernelGGL(k_attn_items, dim3((max_items + 255) / 256), dim3(256), 0, st, g.batch, g.n_kv, g.split,
                      lengths, lane_tab, reinterpret_cast<int4*>(lane_tab + attn_items_offset(g.batch)));
   return hipGetLastError();

@@ -1110,11 +1110,16 @@ static int validate_step(rstr_decoder* d, const int32_t* slots, const int32_t* r
     int32_t L = len[b];
     if (L < 0 || (int64_t)L > (int64_t)d->pps * ps) return fail(s, RSTR_E_INVALID, "lane length out of range");
     if (slots[b] < -1 || slots[b] >= slot_limit) return fail(s, RSTR_E_INVALID, "append slot out of range");
+    // every row (idle ones too) is rotated at its position: the RoPE tables
+    // hold maxpos rows
+    if (pos[b] < 0 || pos[b] >= d->maxpos) return fail(s, RSTR_E_INVALID, "query position outside the decoder's maxpos");
+    // a route starts at a non-negative absolute position (page_pool.clj:647)
+    if (start[b] < 0) return fail(s, RSTR_E_INVALID, "Resident route identity and extents are invalid");
     if (L == 0) {
       if (slots[b] != -1) return fail(s, RSTR_E_INVALID, "inactive lane has an append slot");
       continue;
     }
-    if (pos[b] != start[b] + L - 1 || pos[b] < 0 || pos[b] >= d->maxpos)
+    if ((int64_t)pos[b] != (int64_t)start[b] + L - 1)
       return fail(s, RSTR_E_INVALID, "query position must be the route's last visible token");
     int32_t np = (L + ps - 1) / ps;
     const int32_t* row = pt + (int64_t)b * d->pps;
@@ -1539,6 +1544,33 @@ extern "C" int rstr_append_run(rstr_pool* p, int32_t layer, int32_t batch, const
 }
 
 // ---------------------------------------------------------------------------
+// isolated decode tail
+// ---------------------------------------------------------------------------
+extern "C" int rstr_tail_run(rstr_session* s, int32_t rows, int32_t vocab, int32_t d, const float* logits,
+                             const float* emb, int32_t* tokens_out, float* rows_out) {
+  if (!s) return fail(nullptr, RSTR_E_INVALID, "null session");
+  if (rows <= 0 || vocab <= 0 || d <= 0) return fail(s, RSTR_E_INVALID, "tail extents must be positive");
+  if (!logits || !emb || !tokens_out || !rows_out) return fail(s, RSTR_E_INVALID, "null tail buffer");
+  HIPCHK(s, hipSetDevice(s->device));
+  float *dl = nullptr, *de = nullptr, *dr = nullptr;
+  int32_t* dt = nullptr;
+  hipError_t e = dmalloc(&dl, (size_t)rows * vocab);
+  if (e == hipSuccess) e = dmalloc(&de, (size_t)vocab * d);
+  if (e == hipSuccess) e = dmalloc(&dr, (size_t)rows * d);
+  if (e == hipSuccess) e = dmalloc(&dt, (size_t)rows);
+  if (e == hipSuccess) e = hipMemcpy(dl, logits, sizeof(float) * rows * vocab, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(de, emb, sizeof(float) * vocab * d, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_argmax_gather(s->stream, dl, rows, vocab, de, d, dt, dr);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e == hipSuccess) e = hipMemcpy(tokens_out, dt, sizeof(int32_t) * rows, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(rows_out, dr, sizeof(float) * rows * d, hipMemcpyDeviceToHost);
+  for (void* q : {(void*)dl, (void*)de, (void*)dr, (void*)dt})
+    if (q) hipFree(q);
+  HIPCHK(s, e);
+  return RSTR_OK;
+}
+
+// ---------------------------------------------------------------------------
 // isolated routed attention
 // ---------------------------------------------------------------------------
 struct AttnBufs {
@@ -1601,9 +1633,11 @@ extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, in
     return fail(s, RSTR_E_INVALID, "null attention descriptor");
   for (int b = 0; b <= batch; b++)
     if (row_offsets[b] != b) return fail(s, RSTR_E_INVALID, "row offsets must be 0..batch");
-  for (int b = 0; b < batch; b++)
-    if (lengths && lengths[b] > 0 && positions[b] != start_positions[b] + lengths[b] - 1)
+  for (int b = 0; b < batch; b++) {
+    if (start_positions[b] < 0) return fail(s, RSTR_E_INVALID, "Resident route identity and extents are invalid");
+    if (lengths && lengths[b] > 0 && (int64_t)positions[b] != (int64_t)start_positions[b] + lengths[b] - 1)
       return fail(s, RSTR_E_INVALID, "query position must be the route's last visible token");
+  }
   AttnBufs bf;
   AttnGeom geo;
   int max_items = 0;

@@ -29,7 +29,7 @@ EXPORTS = (
     "rstr_chunk_restore_submit", "rstr_transfer_done", "rstr_transfer_complete", "rstr_chunk_bench", "rstr_decoder_open",
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
     "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_prefill_open",
-    "rstr_prefill_range", "rstr_append_run",
+    "rstr_prefill_range", "rstr_append_run", "rstr_tail_run",
     "rstr_attention_run",
     "rstr_attention_bench", "rstr_schedule_upload", "rstr_schedule_run",
     "rstr_decoder_profile_steps",
@@ -122,6 +122,7 @@ def lib():
             "rstr_prefill_open": (i32, [P, P, i32, i32, i32, i32, C.POINTER(P)]),
             "rstr_prefill_range": (i32, [P, P, P, P, P, i32, i32]),
             "rstr_append_run": (i32, [P, i32, i32, P, P, P]),
+            "rstr_tail_run": (i32, [P, i32, i32, i32, P, P, P, P]),
             "rstr_attention_run": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, P, P, i32, P, P, P]),
             "rstr_attention_bench": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, i32, P, i32,
                                            C.POINTER(f32), C.POINTER(f32)]),
@@ -188,6 +189,19 @@ class Session:
             self.children = []
             lib().rstr_session_close(self.h)
             self.h = None
+
+    def tail(self, logits, emb):
+        """The decode tail on given logits [rows][vocab] and embedding [vocab][d]
+        (decode-tail!): (tokens [rows], gathered rows [rows][d])."""
+        logits, emb = _f32(logits), _f32(emb)
+        rows, vocab = logits.shape
+        d = emb.shape[1]
+        if emb.shape[0] != vocab:
+            raise ValueError("embedding rows differ from the vocabulary")
+        tok = np.empty(rows, np.int32)
+        out = np.empty((rows, d), np.float32)
+        self.check(lib().rstr_tail_run(self.h, rows, vocab, d, _p(logits), _p(emb), _p(tok), _p(out)))
+        return tok, out
 
     def __enter__(self):
         return self

@@ -266,3 +266,31 @@ def step_bytes(cfg: dict, step: dict, weight_bytes: int) -> dict:
         out["kv_unique"] = ukv * L
         out["total_unique"] = weight_bytes + ukv * L + appends + gather
     return out
+
+
+def shared_prefix_routes(B: int, seed: int, page_size: int = 16, mu: float = 7.0, sigma: float = 1.2,
+                         lo: int = 16, hi: int = 32768, shared_frac: float = 0.25):
+    """The isolated-attention workload's routes: B lanes with
+    contexts lognormal(mu, sigma) clipped to [lo, hi], permuted physical page ids,
+    and the first ``shared_frac`` of every lane's full pages taken from one shared
+    run of pages (a common prefix).  Returns (lengths, page_table, physical_pages,
+    shared pages per lane, the generator), the generator positioned after the
+    routes' draws (the workload's queries come next)."""
+    rng = np.random.default_rng(seed)
+    lengths = np.clip(np.rint(np.exp(rng.normal(mu, sigma, B))), lo, hi).astype(np.int32)
+    full = lengths // page_size
+    npages = -(-lengths // page_size)
+    shared_n = np.rint(shared_frac * full).astype(np.int64)
+    S = int(shared_n.max())
+    physical = S + int((npages - shared_n).sum())
+    perm = rng.permutation(physical).astype(np.int32)
+    shared_pages, priv_pages = perm[:S], perm[S:]
+    pt = np.full((B, int(npages.max())), -1, np.int32)
+    used = 0
+    for b in range(B):
+        k = int(shared_n[b])
+        pt[b, :k] = shared_pages[:k]
+        n_priv = int(npages[b]) - k
+        pt[b, k:npages[b]] = priv_pages[used:used + n_priv]
+        used += n_priv
+    return lengths, pt, physical, shared_n, rng

@@ -469,6 +469,20 @@ def test_step_rejects_bad_descriptors(sess):
         bad = dict(good, positions=[3, 0])
         with pytest.raises(hip.RstrError, match="position"):
             d.step_lanes(**bad)
+        # an idle lane's row is still rotated at its position: it must lie in
+        # [0, maxpos) (maxpos 64 here)
+        for p_idle in (64, -3, 1 << 30):
+            with pytest.raises(hip.RstrError, match="maxpos"):
+                d.step_lanes(**dict(good, positions=[0, p_idle]))
+        # a route starts at a non-negative position (page_pool.clj:647), even
+        # when the query position itself is in range
+        bad = dict(good, slots=[2, -1], lengths=[3, 0], start_positions=[-2, 0], positions=[0, 0])
+        with pytest.raises(hip.RstrError, match="extents"):
+            d.step_lanes(**bad)
+        with pytest.raises(hip.RstrError, match="extents"):
+            d.step_lanes(**dict(good, start_positions=[0, -1]))
+        # the decoder still steps after the rejections
+        d.step_lanes(**good)
     finally:
         d.close()
         p.close()
