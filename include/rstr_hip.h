@@ -260,6 +260,22 @@ int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, 
                        int32_t window, float scale, const float* q, const int32_t* row_offsets,
                        const int32_t* positions, const int32_t* page_table, int32_t pages_per_seq,
                        const int32_t* lengths, const int32_t* start_positions, float* out);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): rstr_attention_run's arguments, validation, kernels and
+ * results, with no hipMalloc/hipFree -- the query, descriptors, work tables,
+ * split partials and output are staged in one library-owned device array of
+ * RSTR_ATTN_STATIC_BYTES on each GPU (held until the process ends; its address
+ * is taken when a session opens on that GPU).  A call whose staging would
+ * exceed that size returns RSTR_E_INVALID before any device work.  Every call
+ * on one GPU shares the array and it keeps the last call's contents, so calls
+ * that overlap on one GPU (another thread, another session) race: issue them
+ * from one host thread per device. */
+#define RSTR_ATTN_STATIC_BYTES (64ll << 20)
+int rstr_attention_run_static(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                              int32_t window, float scale, const float* q, const int32_t* row_offsets,
+                              const int32_t* positions, const int32_t* page_table, int32_t pages_per_seq,
+                              const int32_t* lengths, const int32_t* start_positions, float* out);
 /* Timing form of rstr_attention_run: inputs uploaded once, `iters` launches
  * timed with HIP events on the session stream; average ms per launch of the
  * split kernel and of the merge kernel. */

@@ -120,6 +120,11 @@ hipError_t launch_widen(hipStream_t st, int dtype, const void* src, float* dst, 
 // mode 0: pool -> fp16 payload; 1: fp16 payload -> pool; 2: f32 payload -> pool (RNE)
 hipError_t launch_chunk_move(hipStream_t st, int mode, uint16_t** slabs, int nslabs, const int32_t* pages,
                              int start, int count, int page_size, int ept, void* payload);
+// The allocation-free attention entry's staging array (one per GPU) and its
+// device address on the current device (call once per device, device current).
+#define RSTR_STATIC_SCRATCH_BYTES (64ll << 20)
+hipError_t static_scratch_address(void** ptr);
+
 #define RSTR_SYNTH_TEMPLATES 64
 hipError_t launch_gen_templates(hipStream_t st, uint16_t* tmpl, int n_layers, int64_t page_elems,
                                 uint64_t seed);

@@ -1939,3 +1939,18 @@ hipError_t launch_fill_synthetic(hipStream_t st, uint16_t** slabs, int n_layers,
 }
 
 }  // namespace rstr
+
+// ===========================================================================
+// The allocation-free entry's staging: one array per GPU, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel (in host
+// code the name stands for a host-side shadow); it uses the device address
+// that static_scratch_address returns for the current device.
+// ===========================================================================
+namespace rstr {
+static __device__ __align__(256) unsigned char scratch[RSTR_STATIC_SCRATCH_BYTES];
+
+hipError_t static_scratch_address(void** ptr) {
+  *ptr = nullptr;
+  return hipGetSymbolAddress(ptr, HIP_SYMBOL(scratch));
+}
+}  // namespace rstr

@@ -31,7 +31,10 @@ struct rstr_session {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
+  void* scratch = nullptr;  // device address of this GPU's static staging array
 };
+
+static_assert(RSTR_ATTN_STATIC_BYTES == RSTR_STATIC_SCRATCH_BYTES, "one staging size in the ABI and the kernels");
 
 namespace {
 
@@ -191,6 +194,13 @@ extern "C" int rstr_session_open(int32_t device, rstr_session** out) {
   if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess) {
     delete s;
     return fail(nullptr, RSTR_E_HIP, "hipStreamCreate failed");
+  }
+  // the allocation-free entry's staging array of this GPU (its address differs per GPU)
+  hipError_t se = static_scratch_address(&s->scratch);
+  if (se != hipSuccess || !s->scratch) {
+    hipStreamDestroy(s->stream);
+    delete s;
+    return fail(nullptr, RSTR_E_HIP, std::string("static staging address: ") + hipGetErrorString(se));
   }
   *out = s;
   return RSTR_OK;
@@ -1582,9 +1592,9 @@ struct AttnBufs {
   }
 };
 
-static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
-                        int32_t window, const float* q, const int32_t* pt, int32_t pps,
-                        const int32_t* len, AttnBufs& bf, AttnGeom& geo, int* max_items) {
+// Checks shared by the isolated attention entries; returns the longest route.
+static int attn_validate(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split, int32_t window,
+                         const float* q, const int32_t* pt, int32_t pps, const int32_t* len, int64_t* maxlen) {
   rstr_session* s = p->m->s;
   const auto& md = p->m->d;
   if (layer < 0 || layer >= md.n_layers) return fail(s, RSTR_E_INVALID, "layer out of range");
@@ -1596,15 +1606,27 @@ static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q,
   if (window < 0) return fail(s, RSTR_E_INVALID, "invalid window");
   if (!q || !pt || !len) return fail(s, RSTR_E_INVALID, "null attention input");
   int ps = p->page_size;
-  int64_t maxlen = 0;
+  *maxlen = 0;
   for (int b = 0; b < batch; b++) {
     if (len[b] < 0 || (int64_t)len[b] > (int64_t)pps * ps) return fail(s, RSTR_E_INVALID, "length out of range");
     for (int i = 0; i < (len[b] + ps - 1) / ps; i++) {
       int32_t pg = pt[(int64_t)b * pps + i];
       if (pg < 0 || pg >= p->physical_pages) return fail(s, RSTR_E_INVALID, "page table entry out of range");
     }
-    maxlen = std::max<int64_t>(maxlen, len[b]);
+    *maxlen = std::max<int64_t>(*maxlen, len[b]);
   }
+  return RSTR_OK;
+}
+
+static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                        int32_t window, const float* q, const int32_t* pt, int32_t pps,
+                        const int32_t* len, AttnBufs& bf, AttnGeom& geo, int* max_items) {
+  rstr_session* s = p->m->s;
+  const auto& md = p->m->d;
+  int64_t maxlen = 0;
+  int rc = attn_validate(p, layer, batch, n_q, split, window, q, pt, pps, len, &maxlen);
+  if (rc) return rc;
+  int G = n_q / md.n_kv;
   int hd = md.head_dim;
   *max_items = (int)std::max<int64_t>(1, (int64_t)batch * md.n_kv * ((maxlen + split - 1) / split + 1));
   HIPCHK(s, hipSetDevice(s->device));
@@ -1613,7 +1635,7 @@ static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q,
   HIPCHK(s, dmalloc(&bf.part, (size_t)*max_items * G * (hd + 2)));
   HIPCHK(s, dmalloc(&bf.pt, (size_t)batch * pps));
   HIPCHK(s, dmalloc(&bf.len, (size_t)batch));
-  geo = AttnGeom{batch, n_q, md.n_kv, hd, ps, pps, split, window, 0.0f};
+  geo = AttnGeom{batch, n_q, md.n_kv, hd, p->page_size, pps, split, window, 0.0f};
   const size_t tabw = attn_tab_words(geo, *max_items);
   if (tabw == 0) return fail(s, RSTR_E_INVALID, "unsupported attention geometry");
   HIPCHK(s, dmalloc(&bf.tab, tabw));
@@ -1623,12 +1645,8 @@ static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q,
   return RSTR_OK;
 }
 
-extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
-                                  int32_t window, float scale, const float* q, const int32_t* row_offsets,
-                                  const int32_t* positions, const int32_t* page_table, int32_t pps,
-                                  const int32_t* lengths, const int32_t* start_positions, float* out) {
-  if (!p) return fail(nullptr, RSTR_E_INVALID, "null pool");
-  rstr_session* s = p->m->s;
+static int attn_check_rows(rstr_session* s, int32_t batch, const int32_t* row_offsets, const int32_t* positions,
+                           const int32_t* lengths, const int32_t* start_positions, float* out) {
   if (!row_offsets || !positions || !start_positions || !out)
     return fail(s, RSTR_E_INVALID, "null attention descriptor");
   for (int b = 0; b <= batch; b++)
@@ -1638,10 +1656,21 @@ extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, in
     if (lengths && lengths[b] > 0 && (int64_t)positions[b] != (int64_t)start_positions[b] + lengths[b] - 1)
       return fail(s, RSTR_E_INVALID, "query position must be the route's last visible token");
   }
+  return RSTR_OK;
+}
+
+extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                                  int32_t window, float scale, const float* q, const int32_t* row_offsets,
+                                  const int32_t* positions, const int32_t* page_table, int32_t pps,
+                                  const int32_t* lengths, const int32_t* start_positions, float* out) {
+  if (!p) return fail(nullptr, RSTR_E_INVALID, "null pool");
+  rstr_session* s = p->m->s;
+  int rc = attn_check_rows(s, batch, row_offsets, positions, lengths, start_positions, out);
+  if (rc) return rc;
   AttnBufs bf;
   AttnGeom geo;
   int max_items = 0;
-  int rc = attn_prepare(p, layer, batch, n_q, split, window, q, page_table, pps, lengths, bf, geo, &max_items);
+  rc = attn_prepare(p, layer, batch, n_q, split, window, q, page_table, pps, lengths, bf, geo, &max_items);
   if (rc) return rc;
   geo.scale = scale;
   hipStream_t st = s->stream;
@@ -1652,6 +1681,69 @@ extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, in
   HIPCHK(s, launch_attn_merge(st, geo, bf.len, bf.tab, bf.part, bf.out, nullptr));
   HIPCHK(s, hipStreamSynchronize(st));
   HIPCHK(s, hipMemcpy(out, bf.out, sizeof(float) * batch * n_q * geo.hd, hipMemcpyDeviceToHost));
+  return RSTR_OK;
+}
+
+// The same attention with every device buffer carved out of the session GPU's
+// static staging array (256-byte aligned regions); the work list is sized to
+// the routes' exact item count, which changes only how items are spread over
+// waves, never an item's arithmetic.
+extern "C" int rstr_attention_run_static(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, int32_t split,
+                                         int32_t window, float scale, const float* q, const int32_t* row_offsets,
+                                         const int32_t* positions, const int32_t* page_table, int32_t pps,
+                                         const int32_t* lengths, const int32_t* start_positions, float* out) {
+  if (!p) return fail(nullptr, RSTR_E_INVALID, "null pool");
+  rstr_session* s = p->m->s;
+  int rc = attn_check_rows(s, batch, row_offsets, positions, lengths, start_positions, out);
+  if (rc) return rc;
+  int64_t maxlen = 0;
+  if ((rc = attn_validate(p, layer, batch, n_q, split, window, q, page_table, pps, lengths, &maxlen))) return rc;
+  const auto& md = p->m->d;
+  const int hd = md.head_dim, G = n_q / md.n_kv;
+  // exact item count: n_kv items per split of each lane's visible range
+  int64_t items = 0;
+  for (int b = 0; b < batch; b++) {
+    const int64_t L = lengths[b];
+    if (L <= 0) continue;
+    const int64_t lo = window > 0 ? std::max<int64_t>(0, L - window) : 0;
+    items += (int64_t)md.n_kv * ((L - 1) / split - lo / split + 1);
+  }
+  items = std::max<int64_t>(items, 1);
+  if (items > INT32_MAX / 4) return fail(s, RSTR_E_INVALID, "attention work exceeds the static staging maximum");
+  const int max_items = (int)items;
+  AttnGeom geo{batch, n_q, md.n_kv, hd, p->page_size, pps, split, window, scale};
+  const size_t tabw = attn_tab_words(geo, max_items);
+  if (tabw == 0) return fail(s, RSTR_E_INVALID, "unsupported attention geometry");
+  auto al = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+  const size_t qb = sizeof(float) * (size_t)batch * n_q * hd, ptb = sizeof(int32_t) * (size_t)batch * pps,
+               lb = sizeof(int32_t) * (size_t)batch, tb = sizeof(int32_t) * tabw,
+               pb = sizeof(float) * (size_t)max_items * G * (hd + 2);
+  const size_t o_q = 0, o_out = o_q + al(qb), o_pt = o_out + al(qb), o_len = o_pt + al(ptb), o_tab = o_len + al(lb),
+               o_part = o_tab + al(tb), total = o_part + al(pb);
+  if (total > (size_t)RSTR_ATTN_STATIC_BYTES)
+    return fail(s, RSTR_E_INVALID, "attention staging of " + std::to_string(total) +
+                                       " bytes exceeds the static staging maximum of " +
+                                       std::to_string((long long)RSTR_ATTN_STATIC_BYTES) + " bytes");
+  HIPCHK(s, hipSetDevice(s->device));
+  char* base = static_cast<char*>(s->scratch);
+  float* dq = reinterpret_cast<float*>(base + o_q);
+  float* dout = reinterpret_cast<float*>(base + o_out);
+  int32_t* dpt = reinterpret_cast<int32_t*>(base + o_pt);
+  int32_t* dlen = reinterpret_cast<int32_t*>(base + o_len);
+  int32_t* dtab = reinterpret_cast<int32_t*>(base + o_tab);
+  float* dpart = reinterpret_cast<float*>(base + o_part);
+  hipStream_t st = s->stream;
+  const int L = md.n_layers;
+  // the previous call on this session finished before it returned; the copies
+  // complete before the kernels that read them are launched
+  HIPCHK(s, hipMemcpy(dq, q, qb, hipMemcpyHostToDevice));
+  HIPCHK(s, hipMemcpy(dpt, page_table, ptb, hipMemcpyHostToDevice));
+  HIPCHK(s, hipMemcpy(dlen, lengths, lb, hipMemcpyHostToDevice));
+  HIPCHK(s, launch_attn_prep(st, geo, dlen, dtab, max_items));
+  HIPCHK(s, launch_attn_split(st, geo, dq, p->slabs[layer], p->slabs[L + layer], dpt, dtab, dpart, max_items));
+  HIPCHK(s, launch_attn_merge(st, geo, dlen, dtab, dpart, dout, nullptr));
+  HIPCHK(s, hipStreamSynchronize(st));
+  HIPCHK(s, hipMemcpy(out, dout, qb, hipMemcpyDeviceToHost));
   return RSTR_OK;
 }
 

@@ -30,7 +30,7 @@ EXPORTS = (
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
     "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_prefill_open",
     "rstr_prefill_range", "rstr_append_run", "rstr_tail_run",
-    "rstr_attention_run",
+    "rstr_attention_run", "rstr_attention_run_static",
     "rstr_attention_bench", "rstr_schedule_upload", "rstr_schedule_run",
     "rstr_decoder_profile_steps",
 )
@@ -124,6 +124,7 @@ def lib():
             "rstr_append_run": (i32, [P, i32, i32, P, P, P]),
             "rstr_tail_run": (i32, [P, i32, i32, i32, P, P, P, P]),
             "rstr_attention_run": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, P, P, i32, P, P, P]),
+            "rstr_attention_run_static": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, P, P, i32, P, P, P]),
             "rstr_attention_bench": (i32, [P, i32, i32, i32, i32, i32, f32, P, P, i32, P, i32,
                                            C.POINTER(f32), C.POINTER(f32)]),
             "rstr_schedule_upload": (i32, [P, P, i32]),
@@ -362,8 +363,9 @@ class Pool:
         return ms.value
 
     def attention(self, layer, q, page_table, lengths, start_positions=None, positions=None,
-                  window=0, scale=None, split=256):
-        """Isolated routed attention (paged-attention/run!) with f32 q/out."""
+                  window=0, scale=None, split=256, static=False):
+        """Isolated routed attention (paged-attention/run!) with f32 q/out;
+        ``static`` selects the allocation-free entry (rstr_attention_run_static)."""
         c = self.model.cfg
         q = _f32(q)
         B, n_q, hd = q.shape
@@ -376,9 +378,9 @@ class Pool:
         rows = _i32(np.arange(B + 1))
         out = np.empty_like(q)
         scale = c["attn_scale"] if scale is None else scale
-        self.sess.check(lib().rstr_attention_run(self.h, layer, B, n_q, split, window, scale, _p(q),
-                                                 _p(rows), _p(pos), _p(pt), pt.shape[1], _p(lengths),
-                                                 _p(starts), _p(out)))
+        fn = lib().rstr_attention_run_static if static else lib().rstr_attention_run
+        self.sess.check(fn(self.h, layer, B, n_q, split, window, scale, _p(q), _p(rows), _p(pos), _p(pt),
+                           pt.shape[1], _p(lengths), _p(starts), _p(out)))
         return out
 
     def attention_bench(self, layer, q, page_table, lengths, window=0, scale=None, split=256,
