@@ -64,6 +64,7 @@ def lib():
             "orc_normal_fill": (None, [u64, u64, i64, f64, f64, P]),
             "orc_quant_q4": (None, [P, i64, i64, P, P]),
             "orc_quant_q8": (None, [P, i64, i64, P, P]),
+            "orc_act_scale": (f32, [f32]),
             "orc_quant_act": (None, [P, i32, i32, P, P]),
             "orc_qlinear": (None, [i32, P, P, i32, i32, P, P, i32, P]),
             "orc_sumsq": (f32, [P, i32]),

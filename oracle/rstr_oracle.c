@@ -219,7 +219,23 @@ void orc_quant_q8(const float* w, int64_t rows, int64_t cols, int8_t* q, uint16_
 
 /* Activation quantisation, symmetric int8 per 32-element block with an fp32 */
 /* scale (the int8-quantised activation of qlinear-i8, decoder.clj:206-213;  */
-/* block size and rounding: parity unpinned vs Raster).                      */
+/* block size and rounding: parity unpinned vs Raster).  The scale is        */
+/* RN(amax/127) rounded up to a 4-bit significand and kept in [2^-21, 480]:  */
+/* then q*d is an exact fp16 value for every |q| <= 127 (7 + 4 significant   */
+/* bits, at least 2^-24, at most 60960), which lets the linear fold d into    */
+/* its integer block dot exactly.  An all-zero block has d = 0.               */
+float orc_act_scale(float amax) {
+  if (!(amax > 0.0f)) return 0.0f;
+  float d = amax / 127.0f;
+  uint32_t b;
+  memcpy(&b, &d, 4);
+  if (b & 0xFFFFFu) b = (b & ~0xFFFFFu) + 0x100000u;   /* round up to 4 significant bits */
+  memcpy(&d, &b, 4);
+  if (d < 0x1p-21f) d = 0x1p-21f;
+  if (d > 480.0f) d = 480.0f;
+  return d;
+}
+
 void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float* scales) {
   int32_t nb = cols / 32;
   for (int32_t r = 0; r < rows; r++) {
@@ -230,7 +246,7 @@ void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float*
         float a = fabsf(xb[i]);
         if (a > amax) amax = a;
       }
-      float d = amax / 127.0f;
+      float d = orc_act_scale(amax);
       float id = (d != 0.0f) ? 1.0f / d : 0.0f;
       for (int i = 0; i < 32; i++) {
         int v = (int)rintf(xb[i] * id);
@@ -242,12 +258,14 @@ void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float*
 }
 
 /* ------------------------------------------------------------------------ */
-/* Dequantising linear y[r][n] = sum_b isum(r,n,b) * (dw[n,b] * dx[r,b]).    */
+/* Dequantising linear y[r][n] = sum_b (isum(r,n,b) * dx[r,b]) * dw[n,b].    */
 /* Canonical order: the nb blocks (nb % 4 == 0) form 4 contiguous quarters   */
-/* of nb/4 blocks; each quarter accumulates acc = fmaf(isum, dw*dx, acc) in   */
+/* of nb/4 blocks; each quarter accumulates acc = fmaf(isum*dx, dw, acc) in   */
 /* block order from +0; y = (q0 + q1) + (q2 + q3).  isum is the exact integer */
-/* block dot.  Integer dots: pinned by brute force; the whole linear is       */
-/* pinned against a float64 numpy restatement within 1e-5 relative.          */
+/* block dot and isum*dx is exact in fp32 (below 2^23 times a power of two,  */
+/* given the activation scale's 4-bit significand).  Integer dots: pinned by  */
+/* brute force; the whole linear is pinned against a float64 numpy            */
+/* restatement within 1e-5 relative.                                          */
 /* ------------------------------------------------------------------------ */
 static inline float tree64(float* v) {
   for (int w = 1; w < 64; w <<= 1)
@@ -289,8 +307,8 @@ void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out
           int32_t isum = (bits == 4)
                              ? dot_q4((const uint8_t*)wq + ((int64_t)n * nb + b) * 16, xr + 32 * b)
                              : dot_q8((const int8_t*)wq + ((int64_t)n * nb + b) * 32, xr + 32 * b);
-          float s = dw[b] * sr[b];
-          acc = fmaf((float)isum, s, acc);
+          float t = (float)isum * sr[b];   /* exact */
+          acc = fmaf(t, dw[b], acc);
         }
         quarter[q] = acc;
       }

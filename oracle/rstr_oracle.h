@@ -70,6 +70,7 @@ void orc_normal_fill(uint64_t key, uint64_t start, int64_t n, double mean, doubl
 /* ---- block quantisation ------------------------------------------------- */
 void orc_quant_q4(const float* w, int64_t rows, int64_t cols, uint8_t* nib, uint16_t* scales);
 void orc_quant_q8(const float* w, int64_t rows, int64_t cols, int8_t* q, uint16_t* scales);
+float orc_act_scale(float amax);
 void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float* scales);
 void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out, int32_t k_in,
                  const int8_t* xq, const float* xs, int32_t rows, float* y);

@@ -65,6 +65,17 @@ __device__ __forceinline__ float h2f_bits(uint16_t b) {
   return (float)__builtin_bit_cast(_Float16, b);
 }
 
+// Activation block scale: RN(amax/127) rounded up to a 4-bit significand and
+// kept in [2^-21, 480], so q*d is an exact fp16 value for every |q| <= 127
+// (7 + 4 significant bits, at least 2^-24, at most 60960); 0 for amax 0.  The
+// projection folds d into its integer block dot exactly.
+__device__ __forceinline__ float act_scale(float amax) {
+  if (!(amax > 0.0f)) return 0.0f;
+  uint32_t b = __float_as_uint(amax / 127.0f);
+  if (b & 0xFFFFFu) b = (b & ~0xFFFFFu) + 0x100000u;
+  return fminf(fmaxf(__uint_as_float(b), 0x1p-21f), 480.0f);
+}
+
 // ---- counter-based synthetic weights --------------------------------------
 #define RSTR_GOLDEN 0x9E3779B97F4A7C15ull
 __host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {

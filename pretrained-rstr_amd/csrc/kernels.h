@@ -14,7 +14,8 @@
 //   one packed fp16 add; the canonical row-major order is restored on export.)
 //
 //  Quantised activation X[M][K] for the MFMA B operand (Mpad = 16*ceil(M/16)):
-//   fp16 integer values [Mpad/16][nb][g][m%16][8], fp32 block scales [nb][Mpad].
+//   fp16 values q*d [Mpad/16][nb][g][m%16][8] (exact: the block scale d has a
+//   4-bit significand), fp32 block scales d [nb][Mpad].
 //
 //  KV pages per layer and slab: fp16 [page][page_size][n_kv][head_dim]
 //   (the routed-append ABI of doc/serving-architecture.md:178-190).
@@ -32,8 +33,8 @@ struct QTensor {       // one device-resident quantised matrix
 };
 
 struct ActBuf {        // quantised activations in MFMA tile order
-  _Float16* q = nullptr;
-  float* s = nullptr;
+  _Float16* q = nullptr; // q*d per element
+  float* s = nullptr;    // d per (block, row)
   int mpad = 0;
 };
 

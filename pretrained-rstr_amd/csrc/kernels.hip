@@ -134,19 +134,21 @@ hipError_t launch_prescale(hipStream_t st, float* out, const float* in, int64_t 
 }
 
 // ===========================================================================
-// Dequantising linear on MFMA: y[m][n] = sum_b isum(m,n,b) * (dw[n,b]*dx[m,b])
+// Dequantising linear on MFMA: y[m][n] = sum_b (isum(m,n,b) * dx[m,b]) * dw[n,b]
 // ===========================================================================
-// The block dot isum is computed exactly by v_mfma_f32_16x16x32_f16: both
-// operands are small integers (|q_w| <= 8 or 127, |q_x| <= 127) held exactly
-// in fp16, every partial sum is an integer below 2^24, so the fp32 result is
-// the exact integer.  Canonical block order: the nb blocks form 4 contiguous
-// quarters; each quarter accumulates acc = fmaf(isum, dw*dx, acc) in block
-// order from +0; y = (q0 + q1) + (q2 + q3).
+// The activation operand holds q_x*dx in fp16, exact because the activation
+// scale has a 4-bit significand (act_scale).  v_mfma_f32_16x16x32_f16 then
+// returns t = isum*dx exactly: every product q_w*(q_x*dx) is an integer times
+// the power of two under dx's significand, and every partial sum stays below
+// 2^24 of those units, so no addition rounds whatever the MFMA's order.
+// Canonical block order: the nb blocks form 4 contiguous quarters; each
+// quarter accumulates acc = fmaf(t, dw, acc) in block order from +0 (one
+// v_fma_mix_f32 with the fp16 weight scale); y = (q0 + q1) + (q2 + q3).
 //
 // The MFMA takes the weights as the A operand and the activations as B, so a
 // lane's accumulator holds 4 consecutive output columns (n = 4*(lane/16) + r)
-// of one row (m = lane%16): it needs one activation scale per block and row
-// tile, and the 4 weight scales of its columns per block and column tile.
+// of one row (m = lane%16): it needs the 4 weight scales of its columns per
+// block and column tile.
 
 #define RSTR_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -196,10 +198,9 @@ __device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1, uint32_t E) {
 // quarters (split s of 4/NQ); with NQ < 4 the workgroups of one column block
 // write 4/NQ output slices that the consumer combines as (s0+s1) or
 // ((s0+s1)+(s2+s3)).  A chunk is KC blocks (KC = 4, or 1 when a quarter is not
-// a whole number of 4-block groups).  Activation fragments (RT*KC KB) and
-// their scales reach a double-buffered LDS ring by direct-to-LDS DMA, shared
-// by the 4 waves; weights and weight scales stream into registers one chunk
-// ahead.  Row tiles past the batch compute on clamped rows and are never
+// a whole number of 4-block groups).  Activation fragments (RT*KC KB) reach a
+// double-buffered LDS ring by direct-to-LDS DMA, shared by the 4 waves;
+// weights and weight scales stream into registers one chunk ahead.  Row tiles past the batch compute on clamped rows and are never
 // stored, which keeps the hot loop free of branches.
 template <int RT, int CT, int BITS, int NQ, int KC>
 __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W,
@@ -210,9 +211,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
                                                 int m_rows, size_t slice_stride) {
   constexpr int DW = BITS == 4 ? 1 : 2;
   constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
-  constexpr int XS_N = RT * 16 * KC;               // activation scales per chunk
-  constexpr int XS_I = (XS_N + 63) / 64;           // dword DMA instructions for them
-  constexpr int BUF_U4 = ACT_KB * 64 + XS_I * 16;  // u32x4 units per ring buffer
+  constexpr int BUF_U4 = ACT_KB * 64;              // u32x4 units per ring buffer
   constexpr int AI = (ACT_KB + 3) / 4;             // activation DMAs per wave
   __shared__ u32x4 ring[2 * BUF_U4];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -230,13 +229,6 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
   const uint32_t E = opaque_vgpr(0x64006400u);
 
   // per-lane DMA sources and weight offsets (chunk-invariant parts)
-  int xs_off[XS_I];
-#pragma unroll
-  for (int u = 0; u < XS_I; u++) {
-    const int e = (u * 64 + lane) % XS_N;
-    const int kc = e / (16 * RT), n2 = (e / RT) % 16, rt = min(e % RT, mt - 1);
-    xs_off[u] = kc * mpad + row0 + rt * 16 + n2;
-  }
   const _Float16* xsrc[AI];  // wave-uniform bases; each lane adds lane*16 bytes
 #pragma unroll
   for (int i = 0; i < AI; i++) {
@@ -264,13 +256,6 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
       if (ACT_KB % 4 == 0 || a < ACT_KB)
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xsrc[i] + (size_t)ch * KC * 512 + lane * 8),
                                          RSTR_LDS_PTR(base + a * 64), 16, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < XS_I; u++) {
-      if ((u & 3) == wave)
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const void*>(Xs + (size_t)(b_begin + ch * KC) * mpad + xs_off[u]),
-            RSTR_LDS_PTR(base + ACT_KB * 64 + u * 16), 4, 0, 0);
     }
   };
 
@@ -324,7 +309,6 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
 
   auto compute = [&](int buf, const uint32_t (&cw)[CT][KC * DW], const uint32_t (&csc)[CT][KC * 2]) {
     const u32x4* abuf = ring + buf * BUF_U4;
-    const float* xsb = reinterpret_cast<const float*>(abuf + ACT_KB * 64);
 #pragma unroll
     for (int kc = 0; kc < KC; kc++) {
       h8 wv[CT];
@@ -335,19 +319,6 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
         else wv[c] = unpack_q8(cw[c][2 * kc], cw[c][2 * kc + 1], E);
         dwh[c][0] = __builtin_bit_cast(h2, csc[c][2 * kc]);
         dwh[c][1] = __builtin_bit_cast(h2, csc[c][2 * kc + 1]);
-      }
-      float dxv[RT];
-      const float* xr = xsb + (kc * 16 + nn) * RT;
-      if constexpr (RT % 4 == 0) {
-#pragma unroll
-        for (int i = 0; i < RT; i += 4) {
-          const f4 t = *reinterpret_cast<const f4*>(xr + i);
-#pragma unroll
-          for (int e = 0; e < 4; e++) dxv[i + e] = t[e];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < RT; i++) dxv[i] = xr[i];
       }
       // software pipeline: the MFMAs of row tile i+1 issue before the VALU
       // work that consumes the results of row tile i
@@ -370,12 +341,8 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
 #pragma unroll
         for (int c = 0; c < CT; c++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            // s = dw*dx (the mixed-precision fma with +0 gives the same value
-            // as the product up to the sign of a zero, which acc ignores)
-            const float s = __builtin_fmaf((float)dwh[c][r >> 1][r & 1], dxv[i], 0.0f);
-            acc[i][c][r] = __builtin_fmaf(d[c][r], s, acc[i][c][r]);
-          }
+          for (int r = 0; r < 4; r++)
+            acc[i][c][r] = __builtin_fmaf(d[c][r], (float)dwh[c][r >> 1][r & 1], acc[i][c][r]);
       }
     }
   };
@@ -569,7 +536,8 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
 }
 
 // Quantise chunk c of row `row` (valid lanes only store) into the MFMA tile
-// layout.  A 32-element block spans 8 consecutive lanes of one round.
+// layout as fp16 q*d.  A 32-element block spans 8 consecutive lanes of one
+// round.
 __device__ __forceinline__ void quant_store(f4 y, bool valid, int c, int row, int nb, int mpad,
                                             _Float16* __restrict__ Q, float* __restrict__ S) {
   float a = valid ? fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3]))) : 0.0f;
@@ -577,14 +545,14 @@ __device__ __forceinline__ void quant_store(f4 y, bool valid, int c, int row, in
   a = fmaxf(a, xor_lane<2>(a));
   a = fmaxf(a, xor_lane<4>(a));
   if (!valid) return;
-  float d = a / 127.0f;
-  float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  const float d = act_scale(a);
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
   h4 q;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     float v = __builtin_rintf(y[i] * id);
     v = fminf(127.0f, fmaxf(-127.0f, v));
-    q[i] = (_Float16)v;
+    q[i] = (_Float16)(v * d);   // exact: 7 + 4 significant bits
   }
   int b = c >> 3, g = (c & 7) >> 1, s0 = (c & 1) * 4;
   size_t off = ((((size_t)(row >> 4) * nb + b) * 4 + g) * 16 + (row & 15)) * 8 + s0;
@@ -1651,7 +1619,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
     for (int d = 0; d < DPL; d++) a = fmaxf(a, fabsf(O[d]));
 #pragma unroll
     for (int m = 1; m < 32 / DPL; m <<= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
-    const float dq = a / 127.0f;
+    const float dq = act_scale(a);
     const float id = (dq != 0.0f) ? 1.0f / dq : 0.0f;
     const int qd = n_q * HD, nb = qd >> 5;
 #pragma unroll
@@ -1660,7 +1628,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
       float v = __builtin_rintf(O[d] * id);
       v = fminf(127.0f, fmaxf(-127.0f, v));
       const int blk = kcol >> 5, g = (kcol & 31) >> 3, s = kcol & 7;
-      Q[((((size_t)(b >> 4) * nb + blk) * 4 + g) * 16 + (b & 15)) * 8 + s] = (_Float16)v;
+      Q[((((size_t)(b >> 4) * nb + blk) * 4 + g) * 16 + (b & 15)) * 8 + s] = (_Float16)(v * dq);
       if ((kcol & 31) == 0) S[(size_t)blk * mpad + b] = dq;
     }
   }

@@ -109,28 +109,68 @@ def test_q4_ggml_known_block_and_bounds():
     assert sc[0, 0] == 0 and ((nib & 15) == 8).all() and ((nib >> 4) == 8).all()
 
 
-@pytest.mark.parametrize("which", ["q8", "act"])
-def test_symmetric_int8_block_quantisation(which):
+def test_symmetric_int8_q8_block_quantisation():
     w = (RNG.standard_normal((32, 256)) * RNG.uniform(0.01, 10, (32, 1))).astype(np.float32)
-    if which == "q8":
-        q, sc = O.quant_q8(w)
-        d = sc.view(np.float16).astype(np.float64)
-        q = q.reshape(32, 8, 32)
-    else:
-        q, d = O.quant_act(w)
-        q = q.reshape(32, 8, 32)
-        d = d.astype(np.float64)
+    q, sc = O.quant_q8(w)
+    d = sc.view(np.float16).astype(np.float64)
+    q = q.reshape(32, 8, 32)
     assert np.abs(q).max() <= 127
     wb = w.reshape(32, 8, 32).astype(np.float64)
     top = np.abs(wb).argmax(-1)
     assert (np.abs(np.take_along_axis(q, top[..., None], -1)) == 127).all()
     assert (np.abs(wb - q * d[..., None]) <= 0.6 * d[..., None] + 1e-12).all()
-    zq, zs = (O.quant_q8 if which == "q8" else O.quant_act)(np.zeros((1, 32), np.float32))
+    zq, zs = O.quant_q8(np.zeros((1, 32), np.float32))
+    assert (zq == 0).all() and np.asarray(zs).view(np.uint8).max() == 0
+
+
+def _prev4(d: float) -> float:
+    """The largest value below d with a 4-bit significand (d itself has one)."""
+    e = math.floor(math.log2(d))
+    return d - 2.0 ** (e - 4) if d == 2.0 ** e else d - 2.0 ** (e - 3)
+
+
+def test_activation_scale_rounding():
+    """The activation block scale is the smallest value with a 4-bit significand
+    that is >= RN(amax/127), kept in [2^-21, 480]; every q*d with |q| <= 127 is
+    then exact in fp16 (the property the linear relies on)."""
+    amax = np.concatenate([np.exp(RNG.uniform(np.log(1e-9), np.log(1e5), 20000)),
+                           [1e-30, 2.0 ** -21 * 127, 127.0, 60960.0, 1e6, 0.0]]).astype(np.float32)
+    for a in amax:
+        d = O.lib().orc_act_scale(float(a))
+        if a == 0:
+            assert d == 0.0
+            continue
+        base = float(np.float32(a) / np.float32(127))
+        assert 2.0 ** -21 <= d <= 480.0
+        m = d / 2.0 ** math.floor(math.log2(d)) * 8
+        assert m == int(m) and 8 <= m <= 15, (a, d)               # 4 significant bits
+        if 2.0 ** -21 < base <= 480.0:
+            assert _prev4(d) < base <= d                               # the smallest such value
+            assert d < base * 1.125 + 1e-300
+        q = np.arange(-127, 128, dtype=np.float64)
+        assert np.array_equal(np.float16(q * d).astype(np.float64), q * d), d
+    assert O.lib().orc_act_scale(1e-30) == 2.0 ** -21
+    assert O.lib().orc_act_scale(1e6) == 480.0
+
+
+def test_activation_block_quantisation():
+    x = (RNG.standard_normal((32, 256)) * RNG.uniform(0.01, 10, (32, 1))).astype(np.float32)
+    q, d = O.quant_act(x)
+    q = q.reshape(32, 8, 32).astype(np.float64)
+    d = d.astype(np.float64)
+    xb = x.reshape(32, 8, 32).astype(np.float64)
+    assert np.abs(q).max() <= 127
+    top = np.abs(xb).argmax(-1)
+    qt = np.abs(np.take_along_axis(q, top[..., None], -1))
+    assert (qt >= 112).all() and (qt <= 127).all()    # the scale exceeds amax/127 by < 1/8
+    assert (np.abs(xb - q * d[..., None]) <= 0.5 * d[..., None] * (1 + 1e-6)).all()
+    zq, zs = O.quant_act(np.zeros((1, 32), np.float32))
     assert (zq == 0).all() and np.asarray(zs).view(np.uint8).max() == 0
 
 
 def test_qlinear_single_block_is_exact_and_matches_float64():
-    """One nonzero block: y = RN(isum * RN(dw*dx)) exactly.  Random: float64."""
+    """One nonzero block: y = fmaf(isum*dx, dw, 0) = RN(isum * dx * dw) exactly
+    (isum*dx is exact).  Random: float64."""
     k = 128
     w = np.zeros((16, k), np.float32)
     x = np.zeros((3, k), np.float32)
@@ -143,8 +183,9 @@ def test_qlinear_single_block_is_exact_and_matches_float64():
         wint = (np.stack([wq & 15, wq >> 4], -1).reshape(16, k).astype(np.int64) - 8) if bits == 4 \
             else wq.reshape(16, k).astype(np.int64)
         isum = xq.astype(np.int64)[:, 64:96] @ wint[:, 64:96].T
-        s = (ws.view(np.float16)[:, 2].astype(np.float32)[None, :] * xs[:, 2][:, None]).astype(np.float32)
-        assert np.array_equal(y, (isum.astype(np.float32) * s).astype(np.float32))
+        exact = isum.astype(np.float64) * xs[:, 2].astype(np.float64)[:, None] \
+            * ws.view(np.float16)[:, 2].astype(np.float64)[None, :]      # <= 30 significant bits
+        assert np.array_equal(y, exact.astype(np.float32))
     # general case vs float64 (dropped blocks, a transposed operand or a sign
     # error are far outside this tolerance)
     w = RNG.standard_normal((24, 512)).astype(np.float32)

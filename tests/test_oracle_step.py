@@ -19,7 +19,8 @@ written from the reference's op order, not from the oracle's code:
 
 Everything is float64 except the two quantisers the path defines: weights are
 the oracle's packed blocks dequantised exactly, and each linear input is
-int8-quantised per 32-block (d = amax/127, q = rint(x/d)) in float64.  The
+int8-quantised per 32-block (d = amax/127 rounded up to a 4-bit significand,
+q = rint(x/d)) in float64.  The
 oracle runs the same descriptors in its f32-KV mode (the reference CPU path's
 f32 kc/vc, decoder.clj:304-310) and in the fp16-KV product mode.
 
@@ -66,9 +67,14 @@ def dequant(wq: np.ndarray, ws: np.ndarray, bits: int) -> np.ndarray:
 
 
 def quant_act64(x: np.ndarray) -> np.ndarray:
-    """Per-32-block symmetric int8 of a float64 row (decoder.clj:206-213), dequantised."""
+    """Per-32-block symmetric int8 of a float64 row (decoder.clj:206-213), dequantised;
+    the block scale is amax/127 rounded up to a 4-bit significand, kept in
+    [2^-21, 480]."""
     b = x.reshape(-1, 32)
-    d = np.abs(b).max(-1, keepdims=True) / 127.0
+    a = np.abs(b).max(-1, keepdims=True) / 127.0
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    d = np.ceil(a / 2.0 ** (e - 3)) * 2.0 ** (e - 3)
+    d = np.where(a > 0, np.clip(d, 2.0 ** -21, 480.0), 0.0)
     q = np.where(d > 0, np.clip(np.rint(b / np.where(d > 0, d, 1.0)), -127, 127), 0.0)
     return (q * d).reshape(x.shape)
 
