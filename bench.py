@@ -31,11 +31,14 @@ HBM_PEAK_GBS = 8000.0
 
 # attention split per workload (the split fixes the canonical reduction order, so it is a
 # decoder parameter): the largest that still gives every resident wave several items
-SPLITS = {"config5": 256, "config3": 128, "config2": 64, "config4": 256, "prefill5": 256, "chunk5": 256}
+SPLITS = {"config5": 256, "config5_1lane": 64, "config3": 128, "config2": 64, "config4": 256, "prefill5": 256,
+          "chunk5": 256}
 
 WORKLOADS = {
     # name: (model, lanes, page_size, maxpos, prompt range, output range, arrivals/step, seed)
     "config5": ("llama3_8b", 128, 16, 4096 + 512, (128, 4096), (32, 512), 4.0, 5),
+    # the same model and request mix served by one lane (the weight-streaming regime)
+    "config5_1lane": ("llama3_8b", 1, 16, 4096 + 512, (128, 4096), (32, 512), 4.0, 5),
     "config2": ("gemma3_270m", 16, 16, 2048 + 256 + 1, (64, 2048), (256, 256), 0.0, 1),
     # config 3: contexts log-uniform [256, 8192], lanes 0-31 fork one 1024-token prefix
     # (prompt/output None selects the shared-prefix planner)
@@ -344,6 +347,70 @@ def cpu_baseline(cfg: dict, prefix: int, budget_s: float) -> dict:
                       f"({el:.1f} s; oracle model build {build_s:.1f} s untimed)"}
 
 
+def linear_params(cfg: dict) -> tuple[int, int]:
+    """(layer linear parameters over all layers, head parameters)."""
+    d, ff, qd, kvr = cfg["d_model"], cfg["d_ff"], cfg["n_q"] * cfg["head_dim"], cfg["n_kv"] * cfg["head_dim"]
+    return cfg["n_layers"] * (qd * d + 2 * kvr * d + d * qd + 2 * ff * d + d * ff), cfg["vocab"] * d
+
+
+def class_rates(cfg: dict, prof: dict, n_steps: int, prof_plan: list, weight_bytes: int) -> dict:
+    """Per kernel class: ms per step and, where the class has an algorithmic byte
+    or flop count, GB/s and TFLOP/s.  Projections: packed weights and scales once
+    per step, 2 flops per weight per active lane; attention: the visible fp16 K+V
+    (unique pages), 4 * n_q * head_dim flops per visible token and layer."""
+    layer_p, head_p = linear_params(cfg)
+    per_w = (16 + 2) / 32 if cfg["weight_bits"] == 4 else (32 + 2) / 32
+    head_bytes = int(head_p * per_w)
+    rows = float(np.mean([st["active"] for st in prof_plan]))
+    kv = float(np.mean([workload.step_bytes(cfg, st, 0).get("kv_unique", workload.step_bytes(cfg, st, 0)["kv"])
+                        for st in prof_plan]))
+    vis = float(np.mean([sum(workload.step_bytes(cfg, st, 0)["kv_per_layer"]) for st in prof_plan])) / (
+        cfg["n_kv"] * cfg["head_dim"] * 4)
+    work = {"qgemm": (weight_bytes - head_bytes, 2.0 * layer_p * rows),
+            "head": (head_bytes, 2.0 * head_p * rows),
+            "attn_split": (kv, 4.0 * cfg["n_q"] * cfg["head_dim"] * vis)}
+    out = {}
+    for k, (ms_tot, n) in prof.items():
+        ms = ms_tot / n_steps
+        e = {"ms_per_step": round(ms, 4), "launches_per_step": round(n / n_steps, 2)}
+        if k in work and ms > 0:
+            b, f = work[k]
+            e["GB/s"] = round(b / (ms * 1e-3) / 1e9, 1)
+            e["TFLOP/s"] = round(f / (ms * 1e-3) / 1e12, 2)
+            e["bytes_per_step"] = int(b)
+        out[k] = e
+    return out
+
+
+def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, seed, dec, pool) -> dict:
+    """The serving loop in the sense of continuation/benchmark.clj:180-194: every
+    step is planned by the host control plane and run through one
+    rstr_step_lanes call (descriptor upload, step graph, token download), timed
+    per step from the host.  Reported beside the device-resident replay, with the
+    host bookkeeping and the boundary call separated."""
+    dev = workload.LiveDevice(dec, pool)
+    planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed + 1000, arrival_mean=arrivals,
+                                    prompt=prompt, output=output, device=dev)
+    for _ in range(2):  # admissions of the steady-state start, first graph replays
+        planner.plan_step()
+    dev.step_seconds = dev.other_seconds = 0.0
+    host0 = planner.host_seconds
+    times = []
+    for _ in range(args.live_steps):
+        t0 = time.perf_counter()
+        planner.plan_step()
+        times.append(time.perf_counter() - t0)
+    n = len(times)
+    total = sum(times)
+    step_s, other_s = dev.step_seconds, dev.other_seconds
+    return {"steps": n, "ms_per_step_median": round(1e3 * float(np.median(times)), 3),
+            "ms_per_step_mean": round(1e3 * total / n, 3),
+            "tokens_per_s_median": round(lanes / float(np.median(times)), 1) if lanes else None,
+            "rstr_step_lanes_ms": round(1e3 * step_s / n, 3),
+            "fills_copies_primes_ms": round(1e3 * other_s / n, 3),
+            "host_bookkeeping_ms": round(1e3 * ((planner.host_seconds - host0) - step_s - other_s) / n, 3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -356,6 +423,7 @@ def main():
     ap.add_argument("--split", type=int, default=None, help="attention split (default: per workload)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--live-steps", type=int, default=20, help="steps of the live serving loop (0: skip)")
     args = ap.parse_args()
     if args.split is None:
         args.split = SPLITS[args.workload]
@@ -442,10 +510,31 @@ def main():
     qg_ms, qg_n = prof["qgemm"]
     log("profile (ms total / launches): " + ", ".join(f"{k} {v[0]:.2f}/{v[1]}" for k, v in prof.items()))
 
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"attn_split_{args.workload}_traffic.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    classes = class_rates(cfg, prof, args.profile_steps, prof_plan, model.weight_bytes)
+    dominant = max(("qgemm", "head", "attn_split"), key=lambda k: classes[k]["ms_per_step"])
+    if dominant == "attn_split":
+        traffic = None
+        tfile = os.path.join(ROOT, "profiles", f"attn_split_{args.workload}_traffic.json")
+        if os.path.exists(tfile):
+            traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+        roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "kernel": "k_attn_split (paged attention, per layer launch)",
+                    "bytes_per_launch": int(attn_bytes), "avg_launch_ms": round(attn_avg_ms, 4)}
+    else:
+        c = classes[dominant]
+        n_launch = prof[dominant][1] / args.profile_steps
+        gbs = c["GB/s"]
+        roofline = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": ("k_qgemm (dequantising projections, weight streaming)" if dominant == "qgemm"
+                               else "k_qgemm (LM head)"),
+                    "bytes_per_launch": int(c["bytes_per_step"] / n_launch),
+                    "avg_launch_ms": round(c["ms_per_step"] / n_launch, 5)}
+    live = None
+    if args.live_steps > 0 and prompt is not None:
+        live = live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, seed, dec, pool)
+        log("live loop: " + json.dumps(live))
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -462,15 +551,15 @@ def main():
                                 f"(copy-on-write on the first divergent append); {planner.cow_pages} pages copied"),
                    "lanes": lanes, "page_size": ps, "physical_pages": physical,
                    "attention_split": args.split, "parallelism": "1 GPU (replica)"},
-        "roofline": {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_attn_split (paged attention, per layer launch)",
-                     "bytes_per_launch": int(attn_bytes), "avg_launch_ms": round(attn_avg_ms, 4)},
+        "roofline": roofline,
         "step_roofline": {"bytes_per_step": int(step_bytes), "logical_bytes_per_step": int(step_bytes_logical),
                           "achieved_gbs": round(step_gbs, 1), "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "kernel_ms_per_step": {k: round(v[0] / args.profile_steps, 3) for k, v in prof.items()},
+        "kernel_classes": classes,
         "host_bookkeeping_ms_per_step": round(host_ms_step, 3),
     }
+    if live is not None:
+        out["live_loop"] = live
     if not args.no_cpu_baseline:
         try:
             mean_ctx = int(np.mean(prompt)) if prompt is not None else int(np.mean(plan[0]["lengths"]))

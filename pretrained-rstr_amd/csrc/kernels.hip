@@ -278,6 +278,24 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
         const u32x4 s1 = *reinterpret_cast<const u32x4*>(sp + 4);
 #pragma unroll
         for (int k = 0; k < 4; k++) { psc[c][k] = s0[k]; psc[c][4 + k] = s1[k]; }
+      } else if constexpr (KC == 2) {
+        // two blocks of one 4-block group (quarters of an even block count)
+        const int ba = b_begin + b;
+        const int bq = (ba >> 2) - (b_begin >> 2), bb = ba & 3;
+        const uint32_t* wp = wsrc[c] + (size_t)bq * 256 * DW + wlane;
+        const uint32_t* sp = ssrc[c] + (size_t)bq * 32 + slane;
+        if constexpr (DW == 1) {
+          const u32x2 w = *reinterpret_cast<const u32x2*>(wp + bb);
+          pw[c][0] = w[0];
+          pw[c][1] = w[1];
+        } else {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(wp + 2 * bb);
+#pragma unroll
+          for (int k = 0; k < 4; k++) pw[c][k] = w[k];
+        }
+        const u32x4 s = *reinterpret_cast<const u32x4*>(sp + 2 * bb);
+#pragma unroll
+        for (int k = 0; k < 4; k++) psc[c][k] = s[k];
       } else {
         const int ba = b_begin + b;
         const int bq = (ba >> 2) - (b_begin >> 2), bb = ba & 3;

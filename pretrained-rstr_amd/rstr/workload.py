@@ -58,17 +58,68 @@ class RecordingDevice:
         return np.zeros(len(self.cur["slots"]), np.int32)
 
 
+class LiveDevice:
+    """Device protocol implementation that executes each call on the HIP decoder
+    as the control plane makes it (the live serving loop): fills and
+    copy-on-write copies on the pool, primes and one ``rstr_step_lanes`` per step
+    on the decoder.  Seconds spent inside ``rstr_step_lanes`` are accumulated."""
+
+    def __init__(self, decoder, pool, fill_seed: int = 7):
+        self.decoder, self.pool, self.fill_seed = decoder, pool, fill_seed
+        self.cur = None
+        self.step_seconds = 0.0
+        self.other_seconds = 0.0
+
+    def begin(self):
+        self.cur = {"fill_pages": [], "cow_pairs": [], "prime_lanes": [], "prime_tokens": []}
+
+    def end(self):
+        st, self.cur = self.cur, None
+        return st
+
+    def copy_page(self, src, dst):
+        t0 = time.perf_counter()
+        self.pool.copy_page(int(src), int(dst))
+        self.other_seconds += time.perf_counter() - t0
+
+    def fill(self, pages):
+        pages = [int(p) for p in pages]
+        if pages:
+            t0 = time.perf_counter()
+            self.pool.fill_synthetic(pages, self.fill_seed)
+            self.other_seconds += time.perf_counter() - t0
+
+    def prime_rows(self, lane_tokens):
+        if lane_tokens:
+            t0 = time.perf_counter()
+            self.decoder.prime_lanes([lt["lane"] for lt in lane_tokens], [lt["token"] for lt in lane_tokens])
+            self.other_seconds += time.perf_counter() - t0
+
+    def upload(self, desc):
+        self._desc = desc
+
+    def run(self):
+        t0 = time.perf_counter()
+        self._tokens = self.decoder.step_lanes(**self._desc)
+        self.step_seconds += time.perf_counter() - t0
+
+    def download_tokens(self):
+        return self._tokens
+
+
 class ChurnPlanner:
-    """Poisson arrivals, uniform prompt/output lengths, fixed lanes, fixed page pool."""
+    """Poisson arrivals, uniform prompt/output lengths, fixed lanes, fixed page pool.
+    ``device`` executes the plan as it is made (``LiveDevice``); by default the
+    steps are recorded for a device-resident schedule."""
 
     def __init__(self, cfg: dict, batch: int, page_size: int, physical_pages: int, maxpos: int,
                  seed: int, arrival_mean: float = 4.0, prompt=(128, 4096), output=(32, 512),
-                 fill_seed: int = 7, warm_start: bool = True, retain_finished: bool = False):
+                 fill_seed: int = 7, warm_start: bool = True, retain_finished: bool = False, device=None):
         self.cfg, self.batch, self.maxpos = cfg, batch, maxpos
         self.rng = np.random.default_rng(seed)
         self.arrival_mean, self.prompt, self.output = arrival_mean, prompt, output
         self.fill_seed = fill_seed
-        self.rec = RecordingDevice()
+        self.rec = device if device is not None else RecordingDevice()
         self.pool = PagePool(page_size, physical_pages, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"],
                              device=self.rec)
         self.dec = PagedDecoder(self.pool, self.rec, batch_size=batch, maxpos=maxpos)
