@@ -101,6 +101,14 @@ __device__ __forceinline__ float synth_normal(uint64_t key, uint64_t index, doub
   return (float)(mean + std * v);
 }
 
+// Loads of data that a step reads exactly once (quantised weights and their
+// scales): non-temporal, so their lines are the first to leave L2 and the
+// activation tiles that every column tile re-reads stay resident.
+template <class T>
+__device__ __forceinline__ T ld_stream(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
 // ---- wavefront reductions ----------------------------------------------------
 // lane exchange v[lane ^ M]: quad permutes for M < 4 (DPP), the swizzle
 // unit inside 32-lane halves for M < 32, bpermute across halves.
