@@ -91,6 +91,9 @@ struct AttnGeom {
 //       (lane | kv head << 20, t0, t1, item index).
 // max_items bounds the step's items (sum over lanes of n_kv * splits).
 #define RSTR_NCH 260  // chunk counts of one split (split <= 4096 tokens)
+// Split partial of one (item, query head): o[hd], m, l and two pad floats, so
+// every record starts on a 16-byte boundary.  An item holds G such records.
+__host__ __device__ constexpr int attn_part_floats(int hd) { return hd + 4; }
 __host__ __device__ inline int attn_ctl_offset(int batch) { return 6 * batch + 3; }
 __host__ __device__ inline int attn_bucket_offset(int batch) { return 6 * batch + 5; }
 inline int lane_tab_words(int batch) { return 6 * batch + 5 + 2 * RSTR_NCH; }

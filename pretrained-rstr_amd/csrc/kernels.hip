@@ -1065,6 +1065,10 @@ __device__ __forceinline__ int attn_swz(int r) {
 // kernel from 5.1 to 5.5 TB/s at 128 lanes (a plain read of the same pages:
 // 6.1 -> 6.9 TB/s).
 #define RSTR_KV_POLICY 2
+// Split partial stores: written through to memory (the gfx950 `sc1` bit).
+#define RSTR_PART_POLICY 16
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format).
+#define RSTR_BUF_DW3 0x00020000
 
 // Geometry of one work item (all values wave-uniform).
 struct AttnItem {
@@ -1429,22 +1433,50 @@ __global__ __launch_bounds__(64) void k_attn_split(
         o[h][d] = o[h][d] + xor_lane<32>(o[h][d]);
       }
     }
-    float* prt = part + (size_t)gc.idx * G * (HD + 2);
-    if (grp == 0) {
+    // Every lane group now holds the whole partial; group grp writes the
+    // records of heads grp, grp + 4, ... with 16-byte stores from all its
+    // lanes.  The stores are written through (sc1): the partials are read
+    // only by the merge launch, and lines held back in L2 and written back
+    // while the page stream runs cost read bandwidth.
+    {
+      constexpr int PF = attn_part_floats(HD);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(part + (size_t)gc.idx * G * PF, 0, G * PF * 4, RSTR_BUF_DW3);
 #pragma unroll
-      for (int h = 0; h < G; h++) {
-        if constexpr (NP >= 16) {
+      for (int h0 = 0; h0 < G; h0 += 4) {
+        const int h = h0 + grp;
+        if (h < G) {
+          float ov[DPL], mh = mx[h0], lh = l[h0];
 #pragma unroll
-          for (int pp = 0; pp < PPL; pp++)
+          for (int d = 0; d < DPL; d++) ov[d] = o[h0][d];
 #pragma unroll
-            for (int e = 0; e < 8; e++) prt[h * (HD + 2) + (e16 + 16 * pp) * 8 + e] = o[h][pp * 8 + e];
-        } else {
+          for (int k = 1; k < 4 && h0 + k < G; k++) {
+            if (grp == k) {
 #pragma unroll
-          for (int e = 0; e < 4; e++) prt[h * (HD + 2) + e16 * 4 + e] = o[h][e];
-        }
-        if (e16 == 0) {
-          prt[h * (HD + 2) + HD] = mx[h];
-          prt[h * (HD + 2) + HD + 1] = l[h];
+              for (int d = 0; d < DPL; d++) ov[d] = o[h0 + k][d];
+              mh = mx[h0 + k];
+              lh = l[h0 + k];
+            }
+          }
+          const int rb = h * PF * 4;  // record byte offset
+          if constexpr (NP >= 16) {
+#pragma unroll
+            for (int pp = 0; pp < PPL; pp++)
+#pragma unroll
+              for (int q4 = 0; q4 < 2; q4++)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    u32x4{__builtin_bit_cast(uint32_t, ov[pp * 8 + q4 * 4]), __builtin_bit_cast(uint32_t, ov[pp * 8 + q4 * 4 + 1]),
+                          __builtin_bit_cast(uint32_t, ov[pp * 8 + q4 * 4 + 2]), __builtin_bit_cast(uint32_t, ov[pp * 8 + q4 * 4 + 3])},
+                    rs, rb + ((e16 + 16 * pp) * 8 + q4 * 4) * 4, 0, RSTR_PART_POLICY);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__builtin_bit_cast(uint32_t, ov[0]), __builtin_bit_cast(uint32_t, ov[1]),
+                      __builtin_bit_cast(uint32_t, ov[2]), __builtin_bit_cast(uint32_t, ov[3])},
+                rs, rb + e16 * 16, 0, RSTR_PART_POLICY);
+          }
+          if (e16 == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, mh), __builtin_bit_cast(uint32_t, lh)},
+                                                  rs, rb + HD * 4, 0, RSTR_PART_POLICY);
         }
       }
     }
@@ -1592,8 +1624,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
     // splits' o per batch.  w_k = exp(m_k - M) is computed once by lane k mod 64
     // and read from that lane (same value, same order of the fmas below).
     constexpr int C = 16;
-    const int stride = G * (HD + 2);
-    const float* pb = part + (size_t)base * stride + hl * (HD + 2);
+    const int stride = G * attn_part_floats(HD);
+    const float* pb = part + (size_t)base * stride + hl * attn_part_floats(HD);
     float ok[C][DPL];
 #pragma unroll
     for (int j = 0; j < C; j++) {

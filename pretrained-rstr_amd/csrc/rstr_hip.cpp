@@ -967,7 +967,7 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   A(dmalloc(&d->qr, (size_t)batch * d->qd));
   A(dmalloc(&d->gu, (size_t)d->s_gu * batch * 2 * md.d_ff));
   if (head_tail) A(dmalloc(&d->logits, (size_t)batch * md.vocab));
-  A(dmalloc(&d->part, (size_t)d->max_items * G * (md.head_dim + 2)));
+  A(dmalloc(&d->part, (size_t)d->max_items * G * attn_part_floats(md.head_dim)));
   A(dmalloc(&d->rope_cos, (size_t)2 * maxpos * half));
   A(dmalloc(&d->rope_sin, (size_t)2 * maxpos * half));
   A(dmalloc(&d->act.q, (size_t)d->mpad * d->kmax));
@@ -1632,7 +1632,7 @@ static int attn_prepare(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q,
   HIPCHK(s, hipSetDevice(s->device));
   HIPCHK(s, dmalloc(&bf.q, (size_t)batch * n_q * hd));
   HIPCHK(s, dmalloc(&bf.out, (size_t)batch * n_q * hd));
-  HIPCHK(s, dmalloc(&bf.part, (size_t)*max_items * G * (hd + 2)));
+  HIPCHK(s, dmalloc(&bf.part, (size_t)*max_items * G * attn_part_floats(hd)));
   HIPCHK(s, dmalloc(&bf.pt, (size_t)batch * pps));
   HIPCHK(s, dmalloc(&bf.len, (size_t)batch));
   geo = AttnGeom{batch, n_q, md.n_kv, hd, p->page_size, pps, split, window, 0.0f};
@@ -1717,7 +1717,7 @@ extern "C" int rstr_attention_run_static(rstr_pool* p, int32_t layer, int32_t ba
   auto al = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
   const size_t qb = sizeof(float) * (size_t)batch * n_q * hd, ptb = sizeof(int32_t) * (size_t)batch * pps,
                lb = sizeof(int32_t) * (size_t)batch, tb = sizeof(int32_t) * tabw,
-               pb = sizeof(float) * (size_t)max_items * G * (hd + 2);
+               pb = sizeof(float) * (size_t)max_items * G * attn_part_floats(hd);
   const size_t o_q = 0, o_out = o_q + al(qb), o_pt = o_out + al(qb), o_len = o_pt + al(ptb), o_tab = o_len + al(lb),
                o_part = o_tab + al(tb), total = o_part + al(pb);
   if (total > (size_t)RSTR_ATTN_STATIC_BYTES)
