@@ -56,6 +56,8 @@ struct Slices {
 int qgemm_splits(int n, int mpad, int bits);
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride);
+hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                        int splits, size_t slice_stride);
 
 // row kernels
 hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,

@@ -434,6 +434,18 @@ def test_wide_batches_bit_exact(sess, B):
         _close(r)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_one_lane_long_k_weight_streaming(sess, bits):
+    """One lane at Llama-3-8B width (first layer, full vocabulary): the MLP down
+    projection (K = 14336) runs through the weight-streaming GEMV, the other
+    projections through the MFMA tile; tokens and logits equal the oracle's on
+    every step, for Q4 and Q8 weights."""
+    print(f"case one lane llama3_8b q{bits}", flush=True)
+    cfg = configs.with_bits(_cfg("llama3_8b", n_layers=1), bits)
+    r = _run_lanes(sess, cfg, 1, [300], [[0], [0], [0]], split=256, ps=16, pages=40, pps=30, maxpos=400)
+    _close(r)
+
+
 @pytest.mark.parametrize("name,layers", [("llama3_8b", 1), ("gemma3_270m", 6), ("qwen3_06b", 1)])
 def test_config_shapes_first_layers(sess, name, layers):
     """Full-width config shapes (vocabulary included) with the first layers only:
