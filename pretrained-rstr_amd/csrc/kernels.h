@@ -98,6 +98,14 @@ struct AttnGeom {
 __host__ __device__ constexpr int attn_part_floats(int hd) { return hd + 4; }
 __host__ __device__ inline int attn_ctl_offset(int batch) { return 6 * batch + 3; }
 __host__ __device__ inline int attn_bucket_offset(int batch) { return 6 * batch + 5; }
+// Static rounds of an n-item work list over R split waves: every round when
+// the list fits in two, else at least two and all but the last one to two
+// (those are claimed from a counter armed to the returned value times R).
+__host__ __device__ inline int attn_static_rounds(int n, int R) {
+  const int c = (n + R - 1) / R;
+  if (c <= 2) return c;
+  return n / R - 1 > 2 ? n / R - 1 : 2;
+}
 inline int lane_tab_words(int batch) { return 6 * batch + 5 + 2 * RSTR_NCH; }
 inline size_t attn_items_offset(int batch) { return ((size_t)lane_tab_words(batch) + 3) & ~(size_t)3; }
 int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported geometry

@@ -1172,9 +1172,9 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     base[batch] = carry_a;
     fbase[batch] = carry_f;
     pbase[batch] = carry_p;
-    // the split kernel's R waves take max(0, N/R - 1) static rounds; the
-    // counter hands out the rest of the list
-    const int arm = max(0, carry_a / R - 1) * R;
+    // the split kernel's R waves take attn_static_rounds(N, R) static
+    // rounds; the counter hands out the rest of the list
+    const int arm = attn_static_rounds(carry_a, R) * R;
     tab[attn_ctl_offset(batch)] = arm;
     tab[attn_ctl_offset(batch) + 1] = arm;
     // list offsets of the partial items by decreasing chunk count
@@ -1298,11 +1298,19 @@ __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlan
 // placed at the load.
 // Rounds below ks are static; later ones claim the next unclaimed list
 // position from the launch's counter (armed to ks*R), so waves that run ahead
-// take over the tail.  Entry x < 0: the wave's sequence has ended.
+// take over the tail.  Entry x < 0: the wave's sequence has ended.  Claims
+// are device-scope atomics on one word, which serialise: when every wave
+// claims at once (a list of one or two rounds, or a claim for the second
+// round made as each wave starts) they cost more than the imbalance they
+// remove, so such lists are static throughout (attn_static_rounds).
 __device__ __forceinline__ int4 attn_item_fetch(const int4* __restrict__ items, int k, int ks, int n,
                                                 int* __restrict__ ctr) {
   const int R = gridDim.x, w = blockIdx.x;
-  if (k < ks) return items[(size_t)k * R + ((k & 1) ? R - 1 - w : w)];
+  if (k < ks) {
+    const int pos = k * R + ((k & 1) ? R - 1 - w : w);
+    return pos < n ? items[pos] : int4{-1, 0, 0, 0};
+  }
+  if (ks * R >= n) return int4{-1, 0, 0, 0};  // no list position is left to claim
   int v = 0;
   if (threadIdx.x == 0) v = atomicAdd(ctr, 1);
   const int pos = uni(v);
@@ -1366,13 +1374,15 @@ __global__ __launch_bounds__(64) void k_attn_split(
     dma_boff[u] = (uint32_t)(dma_r[u] * kvr + dma_off[u]) * 2u;
   }
 
-  // This wave's work: ks static rounds of the list (ks = N / R - 1, so the
-  // last one to two rounds of items are claimed dynamically), then claims.
+  // This wave's work: ks static rounds of the list, then claims.  Round 0 is
+  // always static: the wave's first entry (list position w) is loaded
+  // together with the item count instead of after it.
+  const int4 first_raw = items[blockIdx.x];
   const int n_tot = uni(*n_items);
-  const int ks = max(0, n_tot / (int)gridDim.x - 1);
-  int pk = 0;  // rounds fetched
-  const int4 first = attn_item_fetch(items, pk++, ks, n_tot, ctr);
-  if (first.x < 0) return;
+  const int ks = attn_static_rounds(n_tot, (int)gridDim.x);
+  int pk = 1;  // rounds fetched
+  if ((int)blockIdx.x >= n_tot) return;
+  const int4 first = first_raw;
 
   // One continuous stream per wave: the positions of an item are its K
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
