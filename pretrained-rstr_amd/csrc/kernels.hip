@@ -638,19 +638,19 @@ struct QgPlan {
 };
 // Tile plan from the padded batch (row tiles) and the requested number of K
 // slices (4/nq).  Measured on MI355X at the decode shapes (N 4096..128256,
-// K 4096/14336): 64-row x 16-column wave tiles above 48 rows, except 32 x 16
-// with four K slices at 49..64 rows (twice the workgroups; QKV, O and down
-// 15-20% faster at 64 rows) and at 65..128 rows for outputs up to 4096 wide
-// (O and down 2-5% faster at 128 rows; QKV at 6144 is not), 32 x 32 for
-// 17..48 rows; up to 16
-// rows, 16 x 16 per quarter (one K quarter per wave: the most waves streaming
-// weights, 20-28% faster than 16 x 32 at 1 and 16 rows), 16 x 64 for
-// one-slice heads.
+// K 4096/14336, weights streamed from HBM): 64-row x 16-column wave tiles
+// above 48 rows, except 32 x 16 with four K slices at 49..96 rows (more
+// workgroups: QKV, O and down 15-20% faster at 64 rows, 6-15% at 80 and 96;
+// from 112 rows the 64-row tile is 2-4% faster again), 32 x 32 for 17..48
+// rows; up to 16 rows, 16 x 16 per quarter (one K quarter per wave: the most
+// waves streaming weights, 20-28% faster than 16 x 32 at 1 and 16 rows),
+// 16 x 64 for one-slice heads.
 QgPlan qg_plan(int mpad, int splits, int bits, int n) {
+  (void)n;
   const int mt_all = mpad / 16;
   QgPlan p{};
   p.nq = 4 / splits;
-  if (p.nq == 1 && (mt_all == 4 || (mt_all <= 8 && mt_all > 4 && n <= 4096))) { p.rt = 2; p.ct = 1; }
+  if (p.nq == 1 && mt_all >= 4 && mt_all <= 6) { p.rt = 2; p.ct = 1; }
   else if (mt_all > 3) { p.rt = 4; p.ct = 1; }
   else if (mt_all > 1) { p.rt = 2; p.ct = 2; }
   else { p.rt = 1; p.ct = p.nq == 1 ? 1 : (p.nq == 4 && bits == 4) ? 4 : 2; }
