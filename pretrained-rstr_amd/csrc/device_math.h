@@ -130,24 +130,65 @@ __device__ __forceinline__ float half_mirror_lane(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
 }
 
+// v + v[lane ^ M] and max(v, v[lane ^ M]).  For M = 16 and 32 one gfx950
+// lane swap (v_permlane16_swap / v_permlane32_swap, both operands copies of
+// v) leaves the pair {v[lo], v[hi]} of lanes lo = min(i, i^M),
+// hi = max(i, i^M) in both lanes, without the LDS crossbar; fp add and max
+// commute, so every lane gets the bits of v + xor_lane<M>(v).  The swap is
+// written in assembly: the compiler folds the builtin with two equal
+// operands into an identity (both results v), which drops the exchange.
+// Hazard checks do not see inside the statement, so it supplies the two wait
+// states a swap needs after a VALU write of its operands (the padding the
+// compiler emits before the builtin's swaps).
+template <int M>
+__device__ __forceinline__ void lane_pair(float v, float& lo, float& hi) {
+  float a = v, b = v;
+  if constexpr (M == 16)
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  else
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  lo = a;
+  hi = b;
+}
+template <int M>
+__device__ __forceinline__ float xor_add(float v) {
+  if constexpr (M == 16 || M == 32) {
+    float a, b;
+    lane_pair<M>(v, a, b);
+    return a + b;
+  } else {
+    return v + xor_lane<M>(v);
+  }
+}
+template <int M>
+__device__ __forceinline__ float xor_max(float v) {
+  if constexpr (M == 16 || M == 32) {
+    float a, b;
+    lane_pair<M>(v, a, b);
+    return fmaxf(a, b);
+  } else {
+    return fmaxf(v, xor_lane<M>(v));
+  }
+}
+
 // xor butterfly: level m combines lanes i and i^m.  Because fp add commutes,
 // both lanes hold the same value and the result is the balanced pairwise tree
 // over lane order.
 __device__ __forceinline__ float wave_tree_sum(float v) {
-  v = v + xor_lane<1>(v);
-  v = v + xor_lane<2>(v);
-  v = v + xor_lane<4>(v);
-  v = v + xor_lane<8>(v);
-  v = v + xor_lane<16>(v);
-  return v + xor_lane<32>(v);
+  v = xor_add<1>(v);
+  v = xor_add<2>(v);
+  v = xor_add<4>(v);
+  v = xor_add<8>(v);
+  v = xor_add<16>(v);
+  return xor_add<32>(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, xor_lane<1>(v));
-  v = fmaxf(v, xor_lane<2>(v));
-  v = fmaxf(v, xor_lane<4>(v));
-  v = fmaxf(v, xor_lane<8>(v));
-  v = fmaxf(v, xor_lane<16>(v));
-  return fmaxf(v, xor_lane<32>(v));
+  v = xor_max<1>(v);
+  v = xor_max<2>(v);
+  v = xor_max<4>(v);
+  v = xor_max<8>(v);
+  v = xor_max<16>(v);
+  return xor_max<32>(v);
 }
 
 }  // namespace rstr

@@ -1647,12 +1647,10 @@ __global__ __launch_bounds__(64) void k_attn_split(
     // ---- item complete: combine lane groups, write the partial ---------------
 #pragma unroll
     for (int h = 0; h < G; h++) {
-      l[h] = l[h] + xor_lane<16>(l[h]);
-      l[h] = l[h] + xor_lane<32>(l[h]);
+      l[h] = xor_add<32>(xor_add<16>(l[h]));
 #pragma unroll
       for (int d = 0; d < DPL; d++) {
-        o[h][d] = o[h][d] + xor_lane<16>(o[h][d]);
-        o[h][d] = o[h][d] + xor_lane<32>(o[h][d]);
+        o[h][d] = xor_add<32>(xor_add<16>(o[h][d]));
       }
     }
     // Every lane group now holds the whole partial; group grp writes the
