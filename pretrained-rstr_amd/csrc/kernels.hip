@@ -1383,6 +1383,13 @@ __global__ __launch_bounds__(64) void k_attn_split(
   int pk = 1;  // rounds fetched
   if ((int)blockIdx.x >= n_tot) return;
   const int4 first = first_raw;
+  // Issue priority by progress: a SIMD's two waves otherwise share issue by
+  // age, so the older one runs ahead through the static rounds and the younger
+  // one sets the launch's end.  Each wave starts at priority 3 and steps down
+  // with every item it completes, so a wave that has fallen behind wins issue
+  // until it catches up (config5: 234 -> 228.5 us per split + merge).
+  __builtin_amdgcn_s_setprio(3);
+  int items_done = 0;
 
   // One continuous stream per wave: the positions of an item are its K
   // chunks, then its V chunks; the producer runs RB-1 positions ahead of the
@@ -1700,6 +1707,9 @@ __global__ __launch_bounds__(64) void k_attn_split(
         }
       }
     }
+    if (++items_done == 1) __builtin_amdgcn_s_setprio(2);
+    else if (items_done == 2) __builtin_amdgcn_s_setprio(1);
+    else if (items_done == 3) __builtin_amdgcn_s_setprio(0);
     if (fqn == 0) break;
     cpos = 0;
     gc = attn_item_make(fq0);
