@@ -1734,6 +1734,236 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #undef RSTR_ATTN_READ_Q
 }
 
+// ---- few-item attention: one workgroup of four waves per item -------------------
+// The same canonical order as k_attn_split, for launches whose whole work list
+// fits in two rounds of resident workgroups (few lanes, short contexts).  There
+// an item's own instruction stream bounds the launch: a single wave spends
+// ~0.85 us of dependent QK/PV work per 16-token chunk.  Here four waves share
+// each item:
+//  - QK: 16 lanes per token (lane j holds pieces j + 16i, i.e. slice j, in
+//    order), so each wave scores 4 tokens of a chunk; the slice tree runs on
+//    bits 3, 2, 1, 0 as in the one-wave kernel;
+//  - the split's max is exchanged through LDS, and all 256 threads run the
+//    exp pass;
+//  - PV: wave g carries lane group g's chains (tokens t = g mod 4 in order)
+//    with 64 lanes of HD/64 dims each; the groups combine as ((0+1)+(2+3))
+//    through LDS, the same sums as the one-wave kernel's lane exchanges.
+// A ring of RB chunks, each filled by all 256 threads' DMAs, streams the
+// item's K then V chunks and drains between items.  Every list position is
+// static (attn_static_rounds gives one or two rounds here), so no claims.
+template <int HD, int G, int RB>
+__global__ __launch_bounds__(256) void k_attn_split_wg(
+    int n_kv, int page_size, int ps_shift, int pps, float scale,
+    const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
+    const int32_t* __restrict__ page_table, const int32_t* __restrict__ n_items,
+    const int4* __restrict__ items, float* __restrict__ part) {
+  constexpr int NP = HD / 8;       // 16-byte pieces per row
+  constexpr int CT = 16;           // tokens per chunk
+  constexpr int CU16 = CT * NP;    // 16-byte units per chunk
+  constexpr int UPT = CU16 / 256;  // DMA units per thread per chunk
+  constexpr int NCL = NP / 16;     // QK pieces per lane
+  constexpr int DPL = HD / 64;     // PV dims per lane
+  constexpr int PF = attn_part_floats(HD);
+  static_assert(UPT >= 1 && NCL >= 1 && DPL >= 2, "head dim 128 or 256");
+  static_assert(RB * CU16 * 16 >= 4 * G * HD * 4, "the group combine fits in the ring");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  u32x4* ring = reinterpret_cast<u32x4*>(smem);                   // [RB][CU16]
+  float* red = reinterpret_cast<float*>(ring + RB * CU16);        // [4][G] wave maxima, then l
+  float* sc = red + 4 * G;                                        // [split][G] scores
+  float* comb = reinterpret_cast<float*>(smem);                   // [4][G][HD] o, after PV
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tt = tid >> 4, j = tid & 15;  // QK: token of the chunk, slice
+  const int kvr = n_kv * HD;
+  const uint32_t row_bytes = (uint32_t)kvr * 2u;
+  const uint32_t page_bytes = (uint32_t)page_size * row_bytes;
+  const int n_tot = uni(*n_items);
+  const int R = gridDim.x, w = blockIdx.x;
+  const int ks = attn_static_rounds(n_tot, R);
+  for (int k = 0; k < ks; k++) {
+    const int pos = k * R + ((k & 1) ? R - 1 - w : w);
+    if (pos >= n_tot) continue;
+    const AttnItem it = attn_item_make(items[pos]);
+    const int npos = 2 * it.nch;
+    // The pages of the item's chunks: every wave loads them once per item
+    // (lane i holds page pg0 + i + 64 k in pgv[k]) and reads each chunk's
+    // page with v_readlane (a lookup per chunk would put a memory latency
+    // before every DMA).
+    const int pg0 = it.T0 >> ps_shift;
+    const int npg = ((it.T0 + (it.nch - 1) * CT) >> ps_shift) - pg0 + 1;
+    const int32_t* prow = page_table + (size_t)it.b * pps + pg0;
+    constexpr int PGV = (RSTR_NCH + 63) / 64;
+    int32_t pgv[PGV];
+#pragma unroll
+    for (int k = 0; k < PGV; k++) pgv[k] = (k == 0 || 64 * k < npg) && lane + 64 * k < npg ? prow[lane + 64 * k] : 0;
+    auto issue = [&](int p) {
+      const bool isk = p < it.nch;
+      const int c = isk ? p : p - it.nch;
+      const int tb = it.T0 + c * CT;
+      const int pi = (tb >> ps_shift) - pg0;
+      int page = __builtin_amdgcn_readlane(pgv[0], pi & 63);
+#pragma unroll
+      for (int k = 1; k < PGV; k++)
+        if ((pi >> 6) == k) page = __builtin_amdgcn_readlane(pgv[k], pi & 63);
+      const char* base = reinterpret_cast<const char*>((isk ? kp : vp) + it.kvh * HD) +
+                         (uint64_t)(uint32_t)page * page_bytes + (uint32_t)(tb & (page_size - 1)) * row_bytes;
+      u32x4* dst = ring + (p % RB) * CU16;
+#pragma unroll
+      for (int u = 0; u < UPT; u++) {
+        const int un = u * 256 + tid;
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const void*>(base + (uint32_t)(un / NP) * row_bytes + (uint32_t)(un % NP) * 16u),
+            RSTR_LDS_PTR(dst + u * 256 + wave * 64), 16, 0, RSTR_KV_POLICY);
+      }
+    };
+    // this thread's query pieces: slice j of each head
+    float qv[G][NCL][8];
+    {
+      const float* qg = q + ((size_t)it.b * (n_kv * G) + it.kvh * G) * HD;
+#pragma unroll
+      for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int i = 0; i < NCL; i++) {
+          const f4 a = *reinterpret_cast<const f4*>(qg + h * HD + 8 * (j + 16 * i));
+          const f4 b4 = *reinterpret_cast<const f4*>(qg + h * HD + 8 * (j + 16 * i) + 4);
+#pragma unroll
+          for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = b4[e]; }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // page ids and the query pieces have arrived
+    for (int p = 0; p < RB - 1 && p < npos; p++) issue(p);
+    float mx[G], o[G][DPL], l[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      mx[h] = -__builtin_inff();
+      l[h] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DPL; d++) o[h][d] = 0.0f;
+    }
+    for (int p = 0; p < npos; p++) {
+      // chunk p has landed for this thread once at most the DMAs of the
+      // positions after it (at most RB - 2) are outstanding; its LDS writes
+      // (scores, exp values) are done before the barrier
+      if (p + RB - 2 < npos) __builtin_amdgcn_s_waitcnt(((UPT * (RB - 2)) & 0xF) | (((UPT * (RB - 2)) >> 4) << 14) | 0x0070);
+      else __builtin_amdgcn_s_waitcnt(0x0070);
+      __asm__ __volatile__("" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // every thread's part of chunk p, and every read of slot (p-1) % RB, is done
+      __asm__ __volatile__("" ::: "memory");
+      if (p + RB - 1 < npos) issue(p + RB - 1);
+      const u32x4* buf = ring + (p % RB) * CU16;
+      if (p < it.nch) {
+        // ---- QK: token tt of chunk p, slice j -----------------------------------
+        const int t = it.T0 + p * CT + tt;
+        const bool valid = t >= it.t0 && t < it.t1;
+        float sv[G];
+#pragma unroll
+        for (int h = 0; h < G; h++) sv[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCL; i++) {
+          const h8 kv = __builtin_bit_cast(h8, buf[tt * NP + j + 16 * i]);
+#pragma unroll
+          for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) sv[h] = __builtin_fmaf(qv[h][i][e], (float)kv[e], sv[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+          // slice tree inside each 16-lane row, all DPP: row_ror:8 is lane
+          // i ^ 8; after that level lanes i and i ^ 8 agree, so row_ror:4
+          // delivers the value of lane i ^ 4
+          float v = sv[h];
+          v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true));
+          v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, true));
+          v = v + xor_lane<2>(v);
+          v = v + xor_lane<1>(v);
+          const float s = v * scale;
+          if (valid) mx[h] = fmaxf(mx[h], s);
+          if (valid && j == 0) sc[(size_t)(t - it.t0) * G + h] = s;
+        }
+        if (p == it.nch - 1) {
+          // ---- softmax numerators over the split --------------------------------
+#pragma unroll
+          for (int h = 0; h < G; h++) {
+            mx[h] = wave_max(mx[h]);
+            if (lane == 0) red[wave * G + h] = mx[h];
+          }
+          // scores and wave maxima are written (LDS only: the V chunks in
+          // flight keep streaming)
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          __asm__ __volatile__("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+          for (int h = 0; h < G; h++) mx[h] = fmaxf(fmaxf(red[h], red[G + h]), fmaxf(red[2 * G + h], red[3 * G + h]));
+          const int nt = it.t1 - it.t0;
+          for (int i = tid; i < nt; i += 256)
+#pragma unroll
+            for (int h = 0; h < G; h++) sc[i * G + h] = dexp(sc[i * G + h] - mx[h]);
+          // the next iteration's barrier orders these writes before PV reads them
+        }
+      } else {
+        // ---- PV: wave g = lane group g, rows r = 4 rd + g of the chunk -------------
+        const int c = p - it.nch;
+        const unsigned char* vb = reinterpret_cast<const unsigned char*>(buf);
+#pragma unroll
+        for (int rd = 0; rd < CT / 4; rd++) {
+          const int r = rd * 4 + wave;
+          const int t = it.T0 + c * CT + r;
+          const bool ok = t >= it.t0 && t < it.t1;
+          float vv[DPL];
+          if constexpr (DPL == 2) {
+            const h2 hv = *reinterpret_cast<const h2*>(vb + r * HD * 2 + lane * DPL * 2);
+            vv[0] = ok ? (float)hv[0] : 0.0f;
+            vv[1] = ok ? (float)hv[1] : 0.0f;
+          } else {
+            const h4 hv = *reinterpret_cast<const h4*>(vb + r * HD * 2 + lane * DPL * 2);
+#pragma unroll
+            for (int e = 0; e < 4; e++) vv[e] = ok ? (float)hv[e] : 0.0f;
+          }
+          const float* ps = sc + (size_t)(ok ? t - it.t0 : 0) * G;
+#pragma unroll
+          for (int h = 0; h < G; h++) {
+            const float pr = ok ? ps[h] : 0.0f;
+            l[h] = l[h] + pr;
+#pragma unroll
+            for (int d = 0; d < DPL; d++) o[h][d] = __builtin_fmaf(pr, vv[d], o[h][d]);
+          }
+        }
+      }
+    }
+    // ---- combine the four groups ((0+1)+(2+3)) and write the partial ------------
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();  // every read of the ring is done: it becomes the combine buffer
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+#pragma unroll
+      for (int d = 0; d < DPL; d++) comb[(wave * G + h) * HD + lane * DPL + d] = o[h][d];
+      if (lane == 0) red[wave * G + h] = l[h];
+    }
+    __syncthreads();
+    float* rec = part + (size_t)it.idx * G * PF;
+    for (int e = tid; e < G * HD / 4; e += 256) {
+      const int h = e / (HD / 4), d4 = (e % (HD / 4)) * 4;
+      f4 out;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        out[i] = (comb[(0 * G + h) * HD + d4 + i] + comb[(1 * G + h) * HD + d4 + i]) +
+                 (comb[(2 * G + h) * HD + d4 + i] + comb[(3 * G + h) * HD + d4 + i]);
+      *reinterpret_cast<f4*>(rec + h * PF + d4) = out;
+    }
+    if (tid < G) {
+      const float* lc = red;
+      float m = mx[0];
+#pragma unroll
+      for (int h = 1; h < G; h++)
+        if (tid == h) m = mx[h];
+      rec[tid * PF + HD] = m;
+      rec[tid * PF + HD + 1] = (lc[tid] + lc[G + tid]) + (lc[2 * G + tid] + lc[3 * G + tid]);
+    }
+    __syncthreads();  // the combine buffer is read before the next item's DMA refills the ring
+  }
+}
+
 // Ring depth: deeper rings keep more rows in flight per wave (fewer waves fit).
 #define RSTR_ATTN_RING 3
 
@@ -1759,7 +1989,31 @@ struct AttnSplit {
   static decltype(&k_attn_split<HD, G, LPT, true, RB>) kernel(const AttnGeom& g) {
     return pg16(g) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
   }
+  // Few-item launches (k_attn_split_wg, one 4-wave workgroup per item): head
+  // dim 128 or 256, whole-page chunks, and a largest work list that fits in
+  // two rounds of resident workgroups.  Its ring is 32 KB deep.
+  static constexpr bool kWG = HD == 128 || HD == 256;
+  static constexpr int RBW = HD == 128 ? 8 : 4;
+  static size_t lds_wg(const AttnGeom& g) {
+    return (size_t)RBW * 16 * (HD / 8) * 16 + sizeof(float) * G * (4 + (size_t)g.split);
+  }
+  static int wg_capacity(const AttnGeom& g) {
+    if constexpr (!kWG) {
+      return 0;
+    } else {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_split_wg<HD, G, RBW>, 256, lds_wg(g)) != hipSuccess)
+        return 0;
+      return device_cus() * n;
+    }
+  }
+  static bool use_wg(const AttnGeom& g, int max_items) {
+    if (!kWG || !pg16(g)) return false;
+    const int cap = wg_capacity(g);
+    return cap > 0 && max_items <= 2 * cap;
+  }
   static int grid(const AttnGeom& g, int max_items) {
+    if (use_wg(g, max_items)) return std::max(1, std::min(wg_capacity(g), max_items));
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel(g), 64, lds(g)) != hipSuccess || n <= 0) n = 2;
     return std::max(1, std::min(device_cus() * n, max_items));
@@ -1772,6 +2026,13 @@ struct AttnSplit {
     int* ctr = tab + attn_ctl_offset(g.batch);
     const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch));
     const int shift = pg16(g) ? __builtin_ctz((unsigned)g.page_size) : 0;
+    if constexpr (kWG) {
+      if (use_wg(g, max_items)) {
+        hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv, g.page_size,
+                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part);
+        return;
+      }
+    }
     hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
                        kp, vp, pt, n_items, items, ctr, part);
   }

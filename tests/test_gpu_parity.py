@@ -285,6 +285,50 @@ def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
         m.close()
 
 
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (128, 16, 8), (128, 8, 1), (256, 4, 1), (256, 8, 8),
+                                         (128, 8, 8)])
+@pytest.mark.parametrize("split,window", [(256, 0), (64, 40)])
+def test_attention_few_and_many_item_kernels_agree(sess, hd, n_q, n_kv, split, window):
+    """Short work lists run one 4-wave workgroup per item, long ones one wave per
+    item.  The same seven lanes run alone (short list) and beside a long eighth
+    lane that reuses their pages (its list forces the one-wave kernel): their
+    outputs agree bit for bit, and with the oracle."""
+    print(f"case attention kernels agree hd{hd} q{n_q} kv{n_kv} split{split} window{window}", flush=True)
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
+               head_dim=hd)
+    B, ps, pages = 7, 16, 96
+    long_len = split * (-(-4200 // n_kv))  # > 4200 items of its own: more than two rounds of workgroups
+    pps = -(-long_len // ps)
+    rng = np.random.default_rng(7 * hd + split + window + n_q)
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        lengths = np.array([1, 0, 17, 255, 256, 100, 233], np.int32)
+        perm = rng.permutation(pages).astype(np.int32)
+        pt = np.full((B + 1, pps), -1, np.int32)
+        used = 0
+        for b in range(B):
+            n = -(-lengths[b] // ps)
+            pt[b, :n] = perm[used:used + n]
+            used += n
+        pt[B, :] = np.arange(pps, dtype=np.int32) % pages
+        q = rng.standard_normal((B + 1, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        few = p.attention(0, q[:B], pt[:B], lengths, window=window, scale=scale, split=split)
+        many = p.attention(0, q, pt, np.append(lengths, np.int32(long_len)), window=window, scale=scale,
+                           split=split)
+        assert np.array_equal(few, many[:B])
+        want = O.attention(q[:B], kp, vp, pt[:B], lengths, window, scale, split)
+        assert np.array_equal(few, want)
+    finally:
+        p.close()
+        m.close()
+
+
 def test_attention_long_shared_routes_match_oracle(sess):
     """Config-4 geometry (32/8 heads, hd 128): long routes (many splits), pages
     shared across lanes (a common prefix run), permuted page ids."""
