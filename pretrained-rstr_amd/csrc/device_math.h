@@ -61,9 +61,6 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) {
   _Float16 h = (_Float16)f;
   return __builtin_bit_cast(uint16_t, h);
 }
-__device__ __forceinline__ float h2f_bits(uint16_t b) {
-  return (float)__builtin_bit_cast(_Float16, b);
-}
 
 // Activation block scale: RN(amax/127) rounded up to a 4-bit significand and
 // kept in [2^-21, 480], so q*d is an exact fp16 value for every |q| <= 127
