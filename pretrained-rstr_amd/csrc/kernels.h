@@ -121,8 +121,11 @@ hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* l
                              ActBuf* out_q);
 
 // tail, priming, pages
+// Segments per row of the tail's first stage; the candidate buffer holds
+// rows * argmax_segments(rows, vocab) (value, index) pairs of int32 words.
+int argmax_segments(int rows, int vocab);
 hipError_t launch_argmax_gather(hipStream_t st, const float* logits, int rows, int vocab,
-                                const float* emb, int d, int32_t* tok, float* r0);
+                                const float* emb, int d, int32_t* tok, float* r0, int32_t* cand);
 hipError_t launch_gather_rows(hipStream_t st, const float* emb, int d, const int32_t* lanes,
                               const int32_t* tokens, int n, float* r0);
 hipError_t launch_append_rows(hipStream_t st, const float* k_rows, const float* v_rows, int rows,

@@ -159,6 +159,7 @@ struct rstr_decoder {
   int32_t* lane_tab = nullptr;                      // [2][tabw] attention work tables
   size_t tabw = 0;                                  // words per work table
   int32_t* tokbuf = nullptr;
+  int32_t* amax_cand = nullptr;  // tail candidates, 2 words per (row, segment)
   int32_t *d_lanes = nullptr, *d_tokens = nullptr;  // priming staging
   // pinned host staging
   int32_t* h_desc = nullptr;
@@ -906,8 +907,8 @@ static void decoder_free(rstr_decoder* d) {
   for (void* q : {(void*)d->r0, (void*)d->xmid, (void*)d->o, (void*)d->yqkv, (void*)d->qr, (void*)d->gu,
                   (void*)d->logits, (void*)d->part, (void*)d->rope_cos, (void*)d->rope_sin,
                   (void*)d->act.q, (void*)d->act.s, (void*)d->desc, (void*)d->lane_tab,
-                  (void*)d->tokbuf, (void*)d->d_lanes, (void*)d->d_tokens, (void*)d->sched_desc,
-                  (void*)d->sched_pages, (void*)d->sched_tok})
+                  (void*)d->tokbuf, (void*)d->amax_cand, (void*)d->d_lanes, (void*)d->d_tokens,
+                  (void*)d->sched_desc, (void*)d->sched_pages, (void*)d->sched_tok})
     if (q) hipFree(q);
   if (d->h_desc) hipHostFree(d->h_desc);
   if (d->h_tok) hipHostFree(d->h_tok);
@@ -978,6 +979,7 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   if (d->tabw == 0 && e == hipSuccess) e = hipErrorInvalidValue;
   A(dmalloc(&d->lane_tab, 2 * d->tabw));
   A(dmalloc(&d->tokbuf, (size_t)batch));
+  A(dmalloc(&d->amax_cand, (size_t)2 * batch * argmax_segments(batch, md.vocab)));
   A(dmalloc(&d->d_lanes, (size_t)batch));
   A(dmalloc(&d->d_tokens, (size_t)batch));
   if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_desc, sizeof(int32_t) * d->desc_words);
@@ -1251,7 +1253,7 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
     return launch_qgemm(st, d->m->head, d->act, B, d->logits, md.vocab, 1, (size_t)B * md.vocab);
   });
   run(RSTR_K_TAIL, [&] {
-    return launch_argmax_gather(st, d->logits, B, md.vocab, d->m->emb, dm, d->tokbuf, d->r0);
+    return launch_argmax_gather(st, d->logits, B, md.vocab, d->m->emb, dm, d->tokbuf, d->r0, d->amax_cand);
   });
   return e;
 }
@@ -1563,18 +1565,19 @@ extern "C" int rstr_tail_run(rstr_session* s, int32_t rows, int32_t vocab, int32
   if (!logits || !emb || !tokens_out || !rows_out) return fail(s, RSTR_E_INVALID, "null tail buffer");
   HIPCHK(s, hipSetDevice(s->device));
   float *dl = nullptr, *de = nullptr, *dr = nullptr;
-  int32_t* dt = nullptr;
+  int32_t *dt = nullptr, *dc = nullptr;
   hipError_t e = dmalloc(&dl, (size_t)rows * vocab);
   if (e == hipSuccess) e = dmalloc(&de, (size_t)vocab * d);
   if (e == hipSuccess) e = dmalloc(&dr, (size_t)rows * d);
   if (e == hipSuccess) e = dmalloc(&dt, (size_t)rows);
+  if (e == hipSuccess) e = dmalloc(&dc, (size_t)2 * rows * argmax_segments(rows, vocab));
   if (e == hipSuccess) e = hipMemcpy(dl, logits, sizeof(float) * rows * vocab, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(de, emb, sizeof(float) * vocab * d, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = launch_argmax_gather(s->stream, dl, rows, vocab, de, d, dt, dr);
+  if (e == hipSuccess) e = launch_argmax_gather(s->stream, dl, rows, vocab, de, d, dt, dr, dc);
   if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
   if (e == hipSuccess) e = hipMemcpy(tokens_out, dt, sizeof(int32_t) * rows, hipMemcpyDeviceToHost);
   if (e == hipSuccess) e = hipMemcpy(rows_out, dr, sizeof(float) * rows * d, hipMemcpyDeviceToHost);
-  for (void* q : {(void*)dl, (void*)de, (void*)dr, (void*)dt})
+  for (void* q : {(void*)dl, (void*)de, (void*)dr, (void*)dt, (void*)dc})
     if (q) hipFree(q);
   HIPCHK(s, e);
   return RSTR_OK;
