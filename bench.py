@@ -424,6 +424,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--live-steps", type=int, default=20, help="steps of the live serving loop (0: skip)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="config5 only: skip the config5_1lane and config2 sub-runs of the default line")
     args = ap.parse_args()
     if args.split is None:
         args.split = SPLITS[args.workload]
@@ -442,6 +444,31 @@ def main():
     if args.workload in CHUNK_WORKLOADS:
         print(json.dumps(chunk_workload(args)), flush=True)
         return
+    out = decode_workload(args)
+    if args.workload == "config5" and not args.no_extra:
+        # the latency end of the lane range and the small-model config, measured in the
+        # same run (the driver records one line): config5's model on one lane, and config2
+        out["other_workloads"] = {}
+        for extra, steps in (("config5_1lane", 100), ("config2", 200)):
+            sub = argparse.Namespace(**vars(args))
+            sub.workload, sub.split, sub.steps, sub.warmup = extra, SPLITS[extra], steps, 10
+            sub.live_steps = min(args.live_steps, 10)
+            sub.no_cpu_baseline = args.no_cpu_baseline or extra == "config5_1lane"
+            sub.cpu_seconds = min(args.cpu_seconds, 6.0)
+            r = decode_workload(sub)
+            if extra == "config5_1lane" and "cpu_baseline" in out:
+                # the oracle's one-lane Llama-3-8B decode is this workload's CPU baseline too
+                r["cpu_baseline"] = dict(out["cpu_baseline"], sample="the config5 line's: "
+                                         + out["cpu_baseline"].get("sample", ""))
+            out["other_workloads"][extra] = {k: r[k] for k in (
+                "value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline", "step_roofline",
+                "kernel_ms_per_step", "kernel_classes", "live_loop", "cpu_baseline") if k in r}
+    print(json.dumps(out), flush=True)
+
+
+def decode_workload(args) -> dict:
+    """One continuous-decode workload of WORKLOADS: plan on the host, replay the
+    device-resident schedule in the timed region, profile, live loop, CPU baseline."""
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
     cfg = configs.MODELS[name]
     pps = -(-maxpos // ps)
@@ -570,7 +597,7 @@ def main():
     pool.close()
     model.close()
     sess.close()
-    print(json.dumps(out), flush=True)
+    return out
 
 
 if __name__ == "__main__":

@@ -56,6 +56,12 @@ struct Slices {
 int qgemm_splits(int n, int mpad, int bits);
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride);
+// Gate/up (w = [gate | up], n = 2*ff) with act(gate)*up quantised into `out`
+// in the epilogue (the fp32 gate/up output is not written); the same bits as
+// launch_qgemm + launch_act_quant.  qgemm_act_fused says where it is used.
+bool qgemm_act_fused(int ff, int mpad);
+hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, int ff, int geglu,
+                            ActBuf& out);
 hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
                         int splits, size_t slice_stride);
 

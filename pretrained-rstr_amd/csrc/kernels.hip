@@ -202,22 +202,38 @@ __device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1, uint32_t E) {
 // double-buffered LDS ring by direct-to-LDS DMA, shared by the 4 waves;
 // weights and weight scales stream into registers one chunk ahead.  Row tiles past the batch compute on clamped rows and are never
 // stored, which keeps the hot loop free of branches.
-template <int RT, int CT, int BITS, int NQ, int KC, bool NT>
-__global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W,
+//
+// ACT (gate/up with the gated activation fused, one K slice): workgroup x
+// owns activation block x of the down projection's input, i.e. gate columns
+// 32x..32x+31 (waves 0, 1) and the same up columns (waves 2, 3).  Every wave
+// runs all four quarters, so y = (q0 + q1) + (q2 + q3) as the sliced path's
+// consumer forms it; the epilogue stages y in LDS and writes
+// act(gate) * up quantised (the rule of k_act_quant) into `ep`, and the fp32
+// gate/up output is never written.
+struct ActEpi {
+  _Float16* q;   // quantised activations of the down projection (MFMA tile order)
+  float* s;      // block scales [nb_out][mpad]
+  int mpad, nb_out, geglu;
+};
+
+template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false>
+__global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __restrict__ W,
                                                 const uint16_t* __restrict__ Ws,
                                                 const _Float16* __restrict__ X,
                                                 const float* __restrict__ Xs, int nb, int nct,
                                                 int mpad, float* __restrict__ Y, int ldy,
-                                                int m_rows, size_t slice_stride) {
+                                                int m_rows, size_t slice_stride, ActEpi ep) {
+  static_assert(!ACT || (RT == 4 && CT == 1 && NQ == 4), "fused activation: 64x16 wave tiles, one K slice");
   constexpr int DW = BITS == 4 ? 1 : 2;
   constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
   constexpr int BUF_U4 = ACT_KB * 64;              // u32x4 units per ring buffer
   constexpr int AI = (ACT_KB + 3) / 4;             // activation DMAs per wave
-  __shared__ u32x4 ring[2 * BUF_U4];
+  constexpr int EPI_U4 = ACT ? RT * 256 : 0;       // epilogue tile: 4 waves x RT*16 rows x 16 floats
+  __shared__ u32x4 ring[2 * BUF_U4 > EPI_U4 ? 2 * BUF_U4 : EPI_U4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nn = lane & 15, g = lane >> 4;
-  const int ct0 = (blockIdx.x * 4 + wave) * CT;
+  const int ct0 = ACT ? (wave >> 1) * (nct >> 1) + 2 * (int)blockIdx.x + (wave & 1) : (blockIdx.x * 4 + wave) * CT;
   const int split = blockIdx.y;
   const int rg = blockIdx.z;
   const int row0 = rg * RT * 16;
@@ -405,6 +421,53 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(const uint32_t* __restrict__ W
   for (int ch = 0; ch < nchunk; ch += 2) {
     chunk(ch, pw0, ps0, pw1, ps1);
     if (ch + 1 < nchunk) chunk(ch + 1, pw1, ps1, pw0, ps0);
+  }
+  if constexpr (ACT) {
+    // y tile -> LDS [wave][row][16 columns], then one thread per (row, 8 columns)
+    // of the 32-column block: hh = act(gate) * up, block amax over its 4 lanes,
+    // quantised as quant_store does, one 16-byte store of q*d
+    float* T = reinterpret_cast<float*>(ring);
+    __syncthreads();  // every wave has finished reading the ring
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+      f4 o;
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[r] = sv0[i][0][r] + (sv1[i][0][r] + acc[i][0][r]);
+      *reinterpret_cast<f4*>(T + ((wave * RT * 16 + i * 16 + nn) * 16 + 4 * g)) = o;
+    }
+    __syncthreads();
+    const int r = tid >> 2, cg = tid & 3;  // row of the tile, 8-column group of the block
+    const float* tg = T + (((cg >> 1) * RT * 16 + r) * 16 + 8 * (cg & 1));
+    const float* tu = tg + 2 * RT * 16 * 16;
+    const f4 g0 = *reinterpret_cast<const f4*>(tg), g1 = *reinterpret_cast<const f4*>(tg + 4);
+    const f4 u0 = *reinterpret_cast<const f4*>(tu), u1 = *reinterpret_cast<const f4*>(tu + 4);
+    float y[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      y[k] = (ep.geglu ? dgelu(g0[k]) : dsilu(g0[k])) * u0[k];
+      y[4 + k] = (ep.geglu ? dgelu(g1[k]) : dsilu(g1[k])) * u1[k];
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) a = fmaxf(a, fabsf(y[k]));
+    a = fmaxf(a, xor_lane<1>(a));
+    a = fmaxf(a, xor_lane<2>(a));
+    const int m = row0 + r;
+    if (m < m_rows) {
+      const float d = act_scale(a);
+      const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+      h8 q;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        float v = __builtin_rintf(y[k] * id);
+        v = fminf(127.0f, fmaxf(-127.0f, v));
+        q[k] = (_Float16)(v * d);  // exact: 7 + 4 significant bits
+      }
+      const int b = blockIdx.x;
+      *reinterpret_cast<h8*>(ep.q + ((((size_t)(m >> 4) * ep.nb_out + b) * 4 + cg) * 16 + (m & 15)) * 8) = q;
+      if (cg == 0) ep.s[(size_t)b * ep.mpad + m] = d;
+    }
+    return;
   }
   float* Yq = Y + (size_t)split * slice_stride;
 #pragma unroll
@@ -689,7 +752,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   const bool once = grid.z == 1;      // every weight is read by one workgroup
 #define RSTR_QG_L(R, C, B, Q, K, N)                                                                     \
   hipLaunchKernelGGL((k_qgemm<R, C, B, Q, K, N>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
-                     x.mpad, y, ldy, m_rows, slice_stride)
+                     x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
 #define RSTR_QG(R, C, B, Q)                                        \
   do {                                                             \
     if (kc4 && once) RSTR_QG_L(R, C, B, Q, 4, true);               \
@@ -718,6 +781,43 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 #undef RSTR_QG_Q
 #undef RSTR_QG
 #undef RSTR_QG_L
+  return hipGetLastError();
+}
+
+// Gate/up with the gated activation fused (k_qgemm<4, 1, BITS, 4, KC, NT, true>):
+// used where the one-slice plan has 64-row tiles and enough workgroups to fill
+// the GPU (ff/32 per 64-row group), since every workgroup then covers all of K.
+bool qgemm_act_fused(int ff, int mpad) {
+  const int mt_all = mpad / 16;
+  if (ff % 32 || mt_all < 4) return false;
+  return (size_t)(ff / 32) * ((mt_all + 3) / 4) >= 768;
+}
+
+hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, int ff, int geglu,
+                            ActBuf& out) {
+  const int nb = w.k / 32;
+  if (w.n != 2 * ff || nb % 4 || !qgemm_act_fused(ff, x.mpad) || out.mpad != x.mpad) return hipErrorInvalidValue;
+  if (w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
+  const int nct = w.n / 16;
+  const dim3 grid(ff / 32, 1, (x.mpad / 16 + 3) / 4);
+  const uint32_t* W = (const uint32_t*)w.w;
+  const bool kc4 = (nb / 4) % 4 == 0;
+  const bool once = grid.z == 1;
+  const ActEpi ep{out.q, out.s, out.mpad, ff / 32, geglu};
+#define RSTR_QA_L(B, K, N)                                                                                   \
+  hipLaunchKernelGGL((k_qgemm<4, 1, B, 4, K, N, true>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
+                     x.mpad, nullptr, 0, m_rows, 0, ep)
+#define RSTR_QA(B)                                  \
+  do {                                              \
+    if (kc4 && once) RSTR_QA_L(B, 4, true);         \
+    else if (kc4) RSTR_QA_L(B, 4, false);           \
+    else if (once) RSTR_QA_L(B, 1, true);           \
+    else RSTR_QA_L(B, 1, false);                    \
+  } while (0)
+  if (w.bits == 4) RSTR_QA(4);
+  else RSTR_QA(8);
+#undef RSTR_QA
+#undef RSTR_QA_L
   return hipGetLastError();
 }
 

@@ -155,6 +155,8 @@ struct rstr_decoder {
   float *gu = nullptr, *logits = nullptr, *part = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;   // [2][maxpos][hd/2]
   ActBuf act;
+  ActBuf act_ff;                                    // down-projection input when gate/up fuses the activation
+  bool fuse_act = false;
   int32_t* desc = nullptr;                          // device descriptors
   int32_t* lane_tab = nullptr;                      // [2][tabw] attention work tables
   size_t tabw = 0;                                  // words per work table
@@ -906,7 +908,8 @@ static void decoder_free(rstr_decoder* d) {
   if (d->graph) hipGraphExecDestroy(d->graph);
   for (void* q : {(void*)d->r0, (void*)d->xmid, (void*)d->o, (void*)d->yqkv, (void*)d->qr, (void*)d->gu,
                   (void*)d->logits, (void*)d->part, (void*)d->rope_cos, (void*)d->rope_sin,
-                  (void*)d->act.q, (void*)d->act.s, (void*)d->desc, (void*)d->lane_tab,
+                  (void*)d->act.q, (void*)d->act.s, (void*)d->act_ff.q, (void*)d->act_ff.s,
+                  (void*)d->desc, (void*)d->lane_tab,
                   (void*)d->tokbuf, (void*)d->amax_cand, (void*)d->d_lanes, (void*)d->d_tokens,
                   (void*)d->sched_desc, (void*)d->sched_pages, (void*)d->sched_tok})
     if (q) hipFree(q);
@@ -966,13 +969,18 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   A(dmalloc(&d->o, (size_t)s_d * batch * md.d_model));
   A(dmalloc(&d->yqkv, (size_t)d->s_qkv * batch * d->nqkv));
   A(dmalloc(&d->qr, (size_t)batch * d->qd));
-  A(dmalloc(&d->gu, (size_t)d->s_gu * batch * 2 * md.d_ff));
+  d->fuse_act = qgemm_act_fused(md.d_ff, d->mpad);
+  if (!d->fuse_act) A(dmalloc(&d->gu, (size_t)d->s_gu * batch * 2 * md.d_ff));
   if (head_tail) A(dmalloc(&d->logits, (size_t)batch * md.vocab));
   A(dmalloc(&d->part, (size_t)d->max_items * G * attn_part_floats(md.head_dim)));
   A(dmalloc(&d->rope_cos, (size_t)2 * maxpos * half));
   A(dmalloc(&d->rope_sin, (size_t)2 * maxpos * half));
   A(dmalloc(&d->act.q, (size_t)d->mpad * d->kmax));
   A(dmalloc(&d->act.s, (size_t)d->mpad * (d->kmax / 32)));
+  if (d->fuse_act) {
+    A(dmalloc(&d->act_ff.q, (size_t)d->mpad * md.d_ff));
+    A(dmalloc(&d->act_ff.s, (size_t)d->mpad * (md.d_ff / 32)));
+  }
   A(dmalloc(&d->desc, (size_t)d->desc_words));
   d->tabw = attn_tab_words(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps, split, 0,
                                      md.attn_scale}, d->max_items);
@@ -989,6 +997,7 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
     return fail(s, RSTR_E_OOM, std::string("decoder allocation: ") + hipGetErrorString(e));
   }
   d->act.mpad = d->mpad;
+  d->act_ff.mpad = d->mpad;
   // RoPE tables: table 0 = global theta, table 1 = local theta; double angles.
   {
     std::vector<float> c((size_t)2 * maxpos * half), sn((size_t)2 * maxpos * half);
@@ -1009,6 +1018,10 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   A(hipMemset(d->r0, 0, sizeof(float) * d->mpad * md.d_model));
   A(hipMemset(d->act.q, 0, sizeof(_Float16) * d->mpad * d->kmax));
   A(hipMemset(d->act.s, 0, sizeof(float) * d->mpad * (d->kmax / 32)));
+  if (d->fuse_act) {
+    A(hipMemset(d->act_ff.q, 0, sizeof(_Float16) * d->mpad * md.d_ff));
+    A(hipMemset(d->act_ff.s, 0, sizeof(float) * d->mpad * (md.d_ff / 32)));
+  }
   A(hipDeviceSynchronize());
   if (e != hipSuccess) {
     decoder_free(d);
@@ -1238,11 +1251,17 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
       return launch_post_attn(st, Slices{d->o, d->s_o, sd}, d->r0, d->xmid, W.post_attn_norm, W.ffn_pre_norm, goff, md.eps, B,
                               dm, d->act);
     });
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.gu, d->act, B, d->gu, 2 * md.d_ff, d->s_gu, sg); });
-    run(RSTR_K_ROWS, [&] {
-      return launch_act_quant(st, Slices{d->gu, d->s_gu, sg}, B, md.d_ff, md.ffn_geglu, d->act);
-    });
-    run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm, d->s_down, sd); });
+    if (d->fuse_act) {
+      // gate/up over all of K per workgroup with act(gate)*up quantised in its epilogue
+      run(RSTR_K_QGEMM, [&] { return launch_qgemm_act(st, W.gu, d->act, B, md.d_ff, md.ffn_geglu, d->act_ff); });
+      run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act_ff, B, d->o, dm, d->s_down, sd); });
+    } else {
+      run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.gu, d->act, B, d->gu, 2 * md.d_ff, d->s_gu, sg); });
+      run(RSTR_K_ROWS, [&] {
+        return launch_act_quant(st, Slices{d->gu, d->s_gu, sg}, B, md.d_ff, md.ffn_geglu, d->act);
+      });
+      run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm, d->s_down, sd); });
+    }
     const float* gnext = (l + 1 < L) ? d->m->layers[l + 1].attn_norm : d->m->final_norm;
     run(RSTR_K_ROWS, [&] {
       return launch_post_ffn(st, Slices{d->o, d->s_down, sd}, d->xmid, d->r0, W.ffn_post_norm, gnext, goff, md.eps, B, dm, d->act);
