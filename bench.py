@@ -32,6 +32,7 @@ HBM_PEAK_GBS = 8000.0
 # attention split per workload (the split fixes the canonical reduction order, so it is a
 # decoder parameter): the fastest of 16..512 measured on MI355X for each workload
 SPLITS = {"config5": 256, "config5_1lane": 64, "config3": 256, "config2": 32, "config4": 256, "prefill5": 256,
+          "config1": 64,
           "chunk5": 256}
 
 WORKLOADS = {
@@ -102,6 +103,108 @@ def attention_workload(args) -> dict:
     pool.close()
     model.close()
     sess.close()
+    return out
+
+
+# the reference CPU path's own configuration:
+# (model, weight bits, prompt tokens, greedy steps, prompt seed)
+CPU_WORKLOADS = {"config1": ("gemma3_270m", 8, 32, 64, 0)}
+
+
+def config1_workload(args) -> dict:
+    """Config 1: Gemma-3-270M-shaped Q8 decoder, one lane, a 32-token prompt of
+    uniform ids (seed 0) primed token by token, then 64 greedy steps -- the run
+    BASELINE.json defines on the reference CPU path.  The HIP decoder runs it
+    through one rstr_step_lanes call per step (host-timed, tok/s = 1000 / median
+    decode-step ms as continuation/benchmark.clj:180-194 reports); the oracle
+    runs the same prompt with f32 K/V (decoder.clj:304-310) on all host cores,
+    reported beside the host's STREAM-triad bandwidth, since one token streams
+    every packed weight from host DRAM."""
+    name, bits, P, G, seed = CPU_WORKLOADS[args.workload]
+    cfg = configs.with_bits(configs.MODELS[name], bits)
+    ps, maxpos, split = 16, P + G, args.split
+    pps = -(-maxpos // ps)
+    prompt = [int(x) for x in np.random.default_rng(seed).integers(0, cfg["vocab"], P)]
+
+    def desc(t):
+        return dict(slots=[(t // ps) * ps + t % ps], row_offsets=[0, 1], positions=[t],
+                    page_table=[list(range(pps))], lengths=[t + 1], start_positions=[0])
+
+    def run(dec):
+        """Prompt token t is the input at position t; the last prompt position's
+        argmax is the first generated token, and every later input is the
+        previous step's argmax (the tail's resident row).  Returns (generated
+        tokens, per-step seconds of the G decode steps)."""
+        out, times = [], []
+        dec.prime_lanes([0], [prompt[0]])
+        for t in range(P + G - 1):
+            t0 = time.perf_counter()
+            tok = int(dec.step_lanes(**desc(t))[0])
+            dt = time.perf_counter() - t0
+            if t + 1 < P:
+                dec.prime_lanes([0], [prompt[t + 1]])
+            else:
+                out.append(tok)
+                times.append(dt)
+        return out, times
+
+    sess = hip.Session(0)
+    model = hip.Model(sess, cfg, seed=1)
+    pool = hip.Pool(model, ps, pps)
+    dec = hip.Decoder(model, pool, 1, pps, maxpos, split)
+    for _ in range(max(1, args.warmup)):
+        run(dec)  # the same positions are rewritten: each run is the full config
+    gpu_tokens, times = run(dec)
+    weight_bytes = model.weight_bytes
+    dec.close()
+    pool.close()
+    model.close()
+    sess.close()
+    med = float(np.median(times))
+    kv_bytes = np.mean([2 * cfg["n_layers"] * (t + 1) * cfg["n_kv"] * cfg["head_dim"] * 2 for t in range(P - 1, P + G - 1)])
+    step_bytes = weight_bytes + kv_bytes
+    gbs = step_bytes / med / 1e9
+    log(f"config1: {G} greedy steps, median {med * 1e3:.3f} ms/step (mean {np.mean(times) * 1e3:.3f}), "
+        f"{step_bytes / 1e6:.1f} MB/step")
+    out = {
+        "metric": METRIC, "value": round(1.0 / med, 1), "unit": "tokens/s", "n_gpus": 1, "steps": G,
+        "warmup": args.warmup, "ms_per_step": round(med * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q8/int8 block dots exact, fp32 accumulate, fp16 KV",
+        "data": "synthetic (seeded random-init weights, uniform prompt ids seed 0)",
+        "config": {"workload": f"config1: {name}-shaped Q8 decoder, 1 lane, {P}-token prompt primed token by token, "
+                               f"{G} greedy steps (one rstr_step_lanes call per step, host-timed median)",
+                   "lanes": 1, "page_size": ps, "attention_split": split, "parallelism": "1 GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole step (packed weights + visible K/V per host-timed step)",
+                     "bytes_per_launch": int(step_bytes), "avg_launch_ms": round(med * 1e3, 4)},
+        "generated_tokens_head": gpu_tokens[:8],
+    }
+    if not args.no_cpu_baseline:
+        try:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle as O  # checker / CPU baseline only
+            om = O.Model(cfg, seed=1)
+            od = O.Decoder(om, 1, ps, pps, pps, maxpos, kv_f16=False, split=split)
+            t0 = time.perf_counter()
+            cpu_tokens, cpu_times = run(od)
+            el = time.perf_counter() - t0
+            od.close()
+            om.close()
+            cpu_med = float(np.median(cpu_times))
+            triad = float(O.lib().orc_stream_triad(1 << 26, 5))
+            cpu_gbs = step_bytes / cpu_med / 1e9
+            agree = sum(int(a == b) for a, b in zip(gpu_tokens, cpu_tokens))
+            out["cpu_baseline"] = {
+                "value": round(1.0 / cpu_med, 2), "unit": "tokens/s", "cores": int(O.lib().orc_num_threads()),
+                "kind": "port",
+                "sample": f"the whole config: {P} prompt + {G} greedy steps ({el:.1f} s), median decode step; "
+                          f"f32 K/V as the reference CPU path keeps them",
+                "host_stream_triad_gbs": round(triad, 1), "achieved_gbs": round(cpu_gbs, 1),
+                "frac_of_triad": round(cpu_gbs / triad, 3) if triad > 0 else None,
+                "greedy_tokens_equal_to_gpu": f"{agree}/{G}"}
+        except Exception as e:  # the baseline must not hide the GPU number
+            out["cpu_baseline"] = {"error": repr(e)}
     return out
 
 
@@ -417,7 +520,7 @@ def main():
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="config5", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + sorted(PREFILL_WORKLOADS)
-                    + sorted(CHUNK_WORKLOADS))
+                    + sorted(CHUNK_WORKLOADS) + sorted(CPU_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--pool-fraction", type=float, default=0.8)
     ap.add_argument("--split", type=int, default=None, help="attention split (default: per workload)")
@@ -425,7 +528,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--live-steps", type=int, default=20, help="steps of the live serving loop (0: skip)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="config5 only: skip the config5_1lane and config2 sub-runs of the default line")
+                    help="config5 only: skip the config5_1lane, config2 and config1 sub-runs of the default line")
     args = ap.parse_args()
     if args.split is None:
         args.split = SPLITS[args.workload]
@@ -443,6 +546,9 @@ def main():
         return
     if args.workload in CHUNK_WORKLOADS:
         print(json.dumps(chunk_workload(args)), flush=True)
+        return
+    if args.workload in CPU_WORKLOADS:
+        print(json.dumps(config1_workload(args)), flush=True)
         return
     out = decode_workload(args)
     if args.workload == "config5" and not args.no_extra:
@@ -463,6 +569,11 @@ def main():
             out["other_workloads"][extra] = {k: r[k] for k in (
                 "value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline", "step_roofline",
                 "kernel_ms_per_step", "kernel_classes", "live_loop", "cpu_baseline") if k in r}
+        sub = argparse.Namespace(**vars(args))
+        sub.workload, sub.warmup, sub.split = "config1", 1, SPLITS["config1"]
+        r = config1_workload(sub)
+        out["other_workloads"]["config1"] = {k: r[k] for k in (
+            "value", "unit", "ms_per_step", "steps", "config", "roofline", "cpu_baseline") if k in r}
     print(json.dumps(out), flush=True)
 
 

@@ -91,6 +91,7 @@ def lib():
             "orc_slab": (P, [P, i32, i32]),
             "orc_last_error": (C.c_char_p, []),
             "orc_num_threads": (C.c_int, []),
+            "orc_stream_triad": (C.c_double, [C.c_int64, C.c_int32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

@@ -19,6 +19,31 @@
 
 static __thread char g_err[256];
 int orc_num_threads(void) { return omp_get_max_threads(); }
+
+/* Host memory bandwidth, STREAM triad form (a[i] = b[i] + s*c[i] over doubles,
+ * 24 bytes per element, all threads, static schedule): best GB/s of `reps`
+ * passes after one untimed pass.  The reference CPU path's decode is bound by
+ * streaming its weights from host DRAM; this is the roof it is compared with. */
+double orc_stream_triad(int64_t n, int32_t reps) {
+  double* a = (double*)malloc(sizeof(double) * (size_t)n);
+  double* b = (double*)malloc(sizeof(double) * (size_t)n);
+  double* c = (double*)malloc(sizeof(double) * (size_t)n);
+  if (!a || !b || !c) { free(a); free(b); free(c); return -1.0; }
+  const double sc = 3.0;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) { a[i] = 0.0; b[i] = 1.0; c[i] = 2.0; }
+  double best = 0.0;
+  for (int32_t r = -1; r < reps; r++) {
+    const double t0 = omp_get_wtime();
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) a[i] = b[i] + sc * c[i];
+    const double dt = omp_get_wtime() - t0;
+    const double gbs = 24.0 * (double)n / dt / 1e9;
+    if (r >= 0 && gbs > best) best = gbs;
+  }
+  free(a); free(b); free(c);
+  return best;
+}
 static void set_err(const char* msg) { snprintf(g_err, sizeof g_err, "%s", msg); }
 const char* orc_last_error(void) { return g_err; }
 

@@ -118,6 +118,7 @@ void orc_fill_synthetic(orc_decoder* d, int32_t page, uint64_t seed);
 void* orc_slab(orc_decoder* d, int32_t slab, int32_t layer);
 const char* orc_last_error(void);
 int orc_num_threads(void);
+double orc_stream_triad(int64_t n, int32_t reps);
 
 #ifdef __cplusplus
 }

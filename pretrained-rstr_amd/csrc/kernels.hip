@@ -785,12 +785,16 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 }
 
 // Gate/up with the gated activation fused (k_qgemm<4, 1, BITS, 4, KC, NT, true>):
-// used where the one-slice plan has 64-row tiles and enough workgroups to fill
-// the GPU (ff/32 per 64-row group), since every workgroup then covers all of K.
+// every workgroup covers all of K, so there are ff/32 workgroups per 64-row
+// group, four resident per CU (128 VGPRs).  Used from 1536 workgroups on (1.5
+// rounds of 256 CUs).  Measured on MI355X, Llama-3-8B shapes: at 512 rows
+// (prefill tiles) the fused launch saves the 117 MB slice round trip of the
+// separate activation kernel, 267 -> 262 ms per 4096-token prompt; at 128 rows
+// (896 workgroups, less than one round) the two forms are equal within 0.3%.
 bool qgemm_act_fused(int ff, int mpad) {
   const int mt_all = mpad / 16;
   if (ff % 32 || mt_all < 4) return false;
-  return (size_t)(ff / 32) * ((mt_all + 3) / 4) >= 768;
+  return (size_t)(ff / 32) * ((mt_all + 3) / 4) >= 1536;
 }
 
 hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, int ff, int geglu,

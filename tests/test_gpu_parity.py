@@ -481,13 +481,14 @@ def test_wide_batches_bit_exact(sess, B):
 @pytest.mark.parametrize("name,d_model,bits,B", [("tiny_llama", 512, 4, 100), ("tiny_gemma", 256, 4, 65),
                                                   ("tiny_qwen", 256, 8, 130), ("tiny_llama", 512, 8, 80)])
 def test_fused_gate_up_activation_bit_exact(sess, name, d_model, bits, B):
-    """Wide feed-forward layers at 65..130 rows take the gate/up launch with the gated
-    activation and its quantisation in the epilogue (one K slice, workgroup = one
-    32-column activation block of gate and up): SiLU and GeLU, Q4 and Q8, 4-block
-    and 1-block chunks (d_model 512 / 256), 2 and 3 row groups; rows and tokens
-    equal the oracle's, which runs gate/up and the activation as separate steps."""
+    """A feed-forward width of 32768 at 65..130 rows (2048..3072 workgroups) takes the
+    gate/up launch with the gated activation and its quantisation in the epilogue
+    (one K slice, workgroup = one 32-column activation block of gate and up): SiLU
+    and GeLU, Q4 and Q8, 4-block and 1-block chunks (d_model 512 / 256), 2 and 3 row
+    groups; rows and tokens equal the oracle's, which runs gate/up and the
+    activation as separate steps."""
     print(f"case fused act {name} d={d_model} q{bits} B={B}", flush=True)
-    cfg = configs.with_bits(_cfg(name, d_model=d_model, d_ff=12288, vocab=512), bits)
+    cfg = configs.with_bits(_cfg(name, d_model=d_model, d_ff=32768, vocab=512), bits)
     rng = np.random.default_rng(B + d_model)
     prefix = [int(x) for x in rng.integers(0, 40, B)]
     sched = [list(range(B)), [b for b in range(B) if b % 3]]
