@@ -216,7 +216,11 @@ struct ActEpi {
   int mpad, nb_out, geglu;
 };
 
-template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false>
+// QB (one K slice, quarters of qs = nb/4 blocks that are not whole 4-block
+// chunks, e.g. K = 640): chunks stay 4-block groups and a quarter ends at
+// whichever block of a chunk closes it, so the loads stay 16 bytes per lane
+// and the chain order is unchanged.
+template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false, bool QB = false>
 __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __restrict__ W,
                                                 const uint16_t* __restrict__ Ws,
                                                 const _Float16* __restrict__ X,
@@ -224,6 +228,7 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
                                                 int mpad, float* __restrict__ Y, int ldy,
                                                 int m_rows, size_t slice_stride, ActEpi ep) {
   static_assert(!ACT || (RT == 4 && CT == 1 && NQ == 4), "fused activation: 64x16 wave tiles, one K slice");
+  static_assert(!QB || (NQ == 4 && KC == 4 && !ACT), "quarters inside chunks: one K slice, 4-block chunks");
   constexpr int DW = BITS == 4 ? 1 : 2;
   constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
   constexpr int BUF_U4 = ACT_KB * 64;              // u32x4 units per ring buffer
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
   const int mt = min(RT, (mpad >> 4) - rg * RT);
   const int nb4 = nb >> 2, qs = nb >> 2;
   const int cpq = qs / KC;
-  const int nchunk = NQ * cpq;
+  const int nchunk = QB ? nb / KC : NQ * cpq;
   const int b_begin = split * NQ * qs;
   const uint32_t E = opaque_vgpr(0x64006400u);
 
@@ -344,7 +349,23 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][c][r] = 0.0f;
 
-  auto compute = [&](int buf, const uint32_t (&cw)[CT][KC * DW], const uint32_t (&csc)[CT][KC * 2]) {
+  // quarter kq complete: q0 -> sv0, sv0 + q1 -> sv0, q2 -> sv1 (the last
+  // quarter stays in acc); y = (q0 + q1) + (q2 + q3)
+  auto end_quarter = [&](int kq) {
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+      for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (kq == 0) sv0[i][c][r] = acc[i][c][r];
+          else if (kq == 1) sv0[i][c][r] = sv0[i][c][r] + acc[i][c][r];
+          else sv1[NQ > 2 ? i : 0][c][r] = acc[i][c][r];
+          acc[i][c][r] = 0.0f;
+        }
+  };
+
+  auto compute = [&](int ch, int buf, const uint32_t (&cw)[CT][KC * DW], const uint32_t (&csc)[CT][KC * 2]) {
     const u32x4* abuf = ring + buf * BUF_U4;
 #pragma unroll
     for (int kc = 0; kc < KC; kc++) {
@@ -381,6 +402,10 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
           for (int r = 0; r < 4; r++)
             acc[i][c][r] = __builtin_fmaf(d[c][r], (float)dwh[c][r >> 1][r & 1], acc[i][c][r]);
       }
+      if constexpr (QB) {
+        const int nb_done = ch * KC + kc + 1;  // blocks of the chain done (wave-uniform)
+        if (nb_done % qs == 0 && nb_done < nb) end_quarter(nb_done / qs - 1);
+      }
     }
   };
 
@@ -392,25 +417,11 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
       load_w(ch + 1, nw, nsc);
       issue_dma(ch + 1, (ch + 1) & 1);
     }
-    compute(ch & 1, cw, csc);
-    if ((ch + 1) % cpq == 0) {
-      // quarter kq complete: q0 -> sv0, sv0 + q1 -> sv0, q2 -> sv1 (the last
-      // quarter stays in acc); y = (q0 + q1) + (q2 + q3)
-      if constexpr (NQ > 1) {
+    compute(ch, ch & 1, cw, csc);
+    if constexpr (NQ > 1 && !QB) {
+      if ((ch + 1) % cpq == 0) {
         const int kq = (ch + 1) / cpq - 1;
-        if (kq < NQ - 1) {
-#pragma unroll
-          for (int i = 0; i < RT; i++)
-#pragma unroll
-            for (int c = 0; c < CT; c++)
-#pragma unroll
-              for (int r = 0; r < 4; r++) {
-                if (kq == 0) sv0[i][c][r] = acc[i][c][r];
-                else if (kq == 1) sv0[i][c][r] = sv0[i][c][r] + acc[i][c][r];
-                else sv1[NQ > 2 ? i : 0][c][r] = acc[i][c][r];
-                acc[i][c][r] = 0.0f;
-              }
-        }
+        if (kq < NQ - 1) end_quarter(kq);
       }
     }
   };
@@ -708,14 +719,18 @@ struct QgPlan {
 // rows; up to 16 rows, 16 x 16 per quarter (one K quarter per wave: the most
 // waves streaming weights, 20-28% faster than 16 x 32 at 1 and 16 rows),
 // 16 x 64 for one-slice heads.
-QgPlan qg_plan(int mpad, int splits, int bits, int n) {
-  (void)n;
+// One-slice heads whose quarters are not whole 4-block chunks (K = 640: the
+// Gemma-3-270M head) run 4-block chunks with in-chunk quarter ends (QB), 16 x 32
+// per wave: 262144 x 640 at 16 rows 55 -> 26 us (Q4), 102 -> 45 us (Q8); at one
+// row 53 -> 22.6 us (Q4), 89 -> 38 us (Q8), against 1-block chunks.
+QgPlan qg_plan(int mpad, int splits, int bits, int nb) {
   const int mt_all = mpad / 16;
   QgPlan p{};
   p.nq = 4 / splits;
   if (p.nq == 1 && mt_all >= 4 && mt_all <= 6) { p.rt = 2; p.ct = 1; }
   else if (mt_all > 3) { p.rt = 4; p.ct = 1; }
   else if (mt_all > 1) { p.rt = 2; p.ct = 2; }
+  else if (p.nq == 4 && (nb / 4) % 4 != 0) { p.rt = 1; p.ct = 2; }
   else { p.rt = 1; p.ct = p.nq == 1 ? 1 : (p.nq == 4 && bits == 4) ? 4 : 2; }
   return p;
 }
@@ -743,7 +758,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   // gate/up 16.0 vs 17.6 us), and at two or more rows it wins everywhere.
   if (x.mpad == 16 && m_rows == 1 && w.k >= 8192 && launch_qgemv(st, w, x, m_rows, y, ldy, splits, slice_stride) == hipSuccess)
     return hipSuccess;
-  const QgPlan p = qg_plan(x.mpad, splits, w.bits, w.n);
+  const QgPlan p = qg_plan(x.mpad, splits, w.bits, nb);
   const int nct = w.n / 16;
   const int mt_all = x.mpad / 16;
   const dim3 grid((nct + 4 * p.ct - 1) / (4 * p.ct), splits, (mt_all + p.rt - 1) / p.rt);
@@ -760,9 +775,20 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
     else if (once) RSTR_QG_L(R, C, B, Q, 1, true);                 \
     else RSTR_QG_L(R, C, B, Q, 1, false);                          \
   } while (0)
+// one K slice: 4-block chunks also where a quarter is not whole chunks (QB)
+#define RSTR_QG_LB(R, C, B, N)                                                                                \
+  hipLaunchKernelGGL((k_qgemm<R, C, B, 4, 4, N, false, true>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
+                     x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
+#define RSTR_QG4(R, C, B)                                          \
+  do {                                                             \
+    if (kc4 && once) RSTR_QG_L(R, C, B, 4, 4, true);               \
+    else if (kc4) RSTR_QG_L(R, C, B, 4, 4, false);                 \
+    else if (once) RSTR_QG_LB(R, C, B, true);                      \
+    else RSTR_QG_LB(R, C, B, false);                               \
+  } while (0)
 #define RSTR_QG_Q(R, C, B)                 \
   do {                                     \
-    if (p.nq == 4) RSTR_QG(R, C, B, 4);    \
+    if (p.nq == 4) RSTR_QG4(R, C, B);      \
     else if (p.nq == 2) RSTR_QG(R, C, B, 2); \
     else RSTR_QG(R, C, B, 1);              \
   } while (0)
@@ -779,6 +805,8 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   else RSTR_QG_T(8);
 #undef RSTR_QG_T
 #undef RSTR_QG_Q
+#undef RSTR_QG4
+#undef RSTR_QG_LB
 #undef RSTR_QG
 #undef RSTR_QG_L
   return hipGetLastError();
