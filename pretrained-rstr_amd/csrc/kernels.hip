@@ -220,7 +220,12 @@ struct ActEpi {
 // chunks, e.g. K = 640): chunks stay 4-block groups and a quarter ends at
 // whichever block of a chunk closes it, so the loads stay 16 bytes per lane
 // and the chain order is unchanged.
-template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false, bool QB = false>
+//
+// PL > 0 (1-block chunks, at most PL of them: short K slices such as K = 640
+// in four slices): every chunk's weights, scales and activation DMA are issued
+// at once and the chain runs after one wait, instead of one dependent memory
+// round trip per block.
+template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false, bool QB = false, int PL = 0>
 __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __restrict__ W,
                                                 const uint16_t* __restrict__ Ws,
                                                 const _Float16* __restrict__ X,
@@ -229,12 +234,14 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
                                                 int m_rows, size_t slice_stride, ActEpi ep) {
   static_assert(!ACT || (RT == 4 && CT == 1 && NQ == 4), "fused activation: 64x16 wave tiles, one K slice");
   static_assert(!QB || (NQ == 4 && KC == 4 && !ACT), "quarters inside chunks: one K slice, 4-block chunks");
+  static_assert(PL == 0 || (KC == 1 && !ACT && !QB), "preloaded chains: 1-block chunks");
   constexpr int DW = BITS == 4 ? 1 : 2;
   constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
   constexpr int BUF_U4 = ACT_KB * 64;              // u32x4 units per ring buffer
   constexpr int AI = (ACT_KB + 3) / 4;             // activation DMAs per wave
   constexpr int EPI_U4 = ACT ? RT * 256 : 0;       // epilogue tile: 4 waves x RT*16 rows x 16 floats
-  __shared__ u32x4 ring[2 * BUF_U4 > EPI_U4 ? 2 * BUF_U4 : EPI_U4];
+  constexpr int NBUF = PL > 2 ? PL : 2;            // ring buffers (one per chunk when preloading)
+  __shared__ u32x4 ring[NBUF * BUF_U4 > EPI_U4 ? NBUF * BUF_U4 : EPI_U4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nn = lane & 15, g = lane >> 4;
@@ -426,12 +433,32 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
     }
   };
 
-  uint32_t pw0[CT][KC * DW], ps0[CT][KC * 2], pw1[CT][KC * DW], ps1[CT][KC * 2];
-  load_w(0, pw0, ps0);
-  issue_dma(0, 0);
-  for (int ch = 0; ch < nchunk; ch += 2) {
-    chunk(ch, pw0, ps0, pw1, ps1);
-    if (ch + 1 < nchunk) chunk(ch + 1, pw1, ps1, pw0, ps0);
+  if constexpr (PL > 0) {
+    uint32_t pwa[PL][CT][KC * DW], psa[PL][CT][KC * 2];
+#pragma unroll
+    for (int c = 0; c < PL; c++)
+      if (c < nchunk) {
+        load_w(c, pwa[c], psa[c]);
+        issue_dma(c, c);
+      }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of every chunk
+    __syncthreads();                     // every wave's DMAs have landed
+#pragma unroll
+    for (int c = 0; c < PL; c++)
+      if (c < nchunk) {
+        compute(c, c, pwa[c], psa[c]);
+        if constexpr (NQ > 1) {
+          if ((c + 1) % cpq == 0 && (c + 1) / cpq - 1 < NQ - 1) end_quarter((c + 1) / cpq - 1);
+        }
+      }
+  } else {
+    uint32_t pw0[CT][KC * DW], ps0[CT][KC * 2], pw1[CT][KC * DW], ps1[CT][KC * 2];
+    load_w(0, pw0, ps0);
+    issue_dma(0, 0);
+    for (int ch = 0; ch < nchunk; ch += 2) {
+      chunk(ch, pw0, ps0, pw1, ps1);
+      if (ch + 1 < nchunk) chunk(ch + 1, pw1, ps1, pw0, ps0);
+    }
   }
   if constexpr (ACT) {
     // y tile -> LDS [wave][row][16 columns], then one thread per (row, 8 columns)
@@ -765,13 +792,19 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   const uint32_t* W = (const uint32_t*)w.w;
   const bool kc4 = (nb / 4) % 4 == 0;  // quarters are whole 4-block chunks
   const bool once = grid.z == 1;      // every weight is read by one workgroup
+  const bool pre = !kc4 && (4 / splits) * (nb / 4) <= 8;  // 1-block chunks, all preloaded
 #define RSTR_QG_L(R, C, B, Q, K, N)                                                                     \
   hipLaunchKernelGGL((k_qgemm<R, C, B, Q, K, N>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
                      x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
+#define RSTR_QG_LP(R, C, B, Q, N)                                                                              \
+  hipLaunchKernelGGL((k_qgemm<R, C, B, Q, 1, N, false, false, 8>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, \
+                     nct, x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
 #define RSTR_QG(R, C, B, Q)                                        \
   do {                                                             \
     if (kc4 && once) RSTR_QG_L(R, C, B, Q, 4, true);               \
     else if (kc4) RSTR_QG_L(R, C, B, Q, 4, false);                 \
+    else if (pre && once) RSTR_QG_LP(R, C, B, Q, true);            \
+    else if (pre) RSTR_QG_LP(R, C, B, Q, false);                   \
     else if (once) RSTR_QG_L(R, C, B, Q, 1, true);                 \
     else RSTR_QG_L(R, C, B, Q, 1, false);                          \
   } while (0)
@@ -808,6 +841,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 #undef RSTR_QG4
 #undef RSTR_QG_LB
 #undef RSTR_QG
+#undef RSTR_QG_LP
 #undef RSTR_QG_L
   return hipGetLastError();
 }
