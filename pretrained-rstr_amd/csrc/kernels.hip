@@ -221,10 +221,10 @@ struct ActEpi {
 // whichever block of a chunk closes it, so the loads stay 16 bytes per lane
 // and the chain order is unchanged.
 //
-// PL > 0 (1-block chunks, at most PL of them: short K slices such as K = 640
-// in four slices): every chunk's weights, scales and activation DMA are issued
-// at once and the chain runs after one wait, instead of one dependent memory
-// round trip per block.
+// PL > 0 (at most PL chunks: short K slices such as K = 640 in four slices, or
+// 16-row tiles over 4..8 chunks of 4 blocks): every chunk's weights, scales and
+// activation DMA are issued at once and the chain runs after one wait, instead
+// of one dependent memory round trip per chunk.
 template <int RT, int CT, int BITS, int NQ, int KC, bool NT, bool ACT = false, bool QB = false, int PL = 0>
 __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __restrict__ W,
                                                 const uint16_t* __restrict__ Ws,
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256, ACT ? 4 : 2) void k_qgemm(const uint32_t* __re
                                                 int m_rows, size_t slice_stride, ActEpi ep) {
   static_assert(!ACT || (RT == 4 && CT == 1 && NQ == 4), "fused activation: 64x16 wave tiles, one K slice");
   static_assert(!QB || (NQ == 4 && KC == 4 && !ACT), "quarters inside chunks: one K slice, 4-block chunks");
-  static_assert(PL == 0 || (KC == 1 && !ACT && !QB), "preloaded chains: 1-block chunks");
+  static_assert(PL == 0 || (!ACT && !QB && (KC == 1 || RT == 1)), "preloaded chains: 1-block chunks or 16-row tiles");
   constexpr int DW = BITS == 4 ? 1 : 2;
   constexpr int ACT_KB = RT * KC;                  // 1 KB activation fragments per chunk
   constexpr int BUF_U4 = ACT_KB * 64;              // u32x4 units per ring buffer
@@ -773,6 +773,62 @@ int qgemm_splits(int n, int mpad, int bits) {
   return 4;
 }
 
+// Launch arguments of one projection and the chunking choices made for it.
+struct QgLaunch {
+  dim3 grid;
+  hipStream_t st;
+  const uint32_t* W;
+  const uint16_t* Ws;
+  const _Float16* X;
+  const float* Xs;
+  int nb, nct, mpad;
+  float* y;
+  int ldy, m_rows;
+  size_t slice_stride;
+  bool kc4, once, pre, pre4;
+};
+
+template <int R, int C, int B, int Q, int K, bool N, bool QB, int PL>
+static void qg_go(const QgLaunch& a) {
+  hipLaunchKernelGGL((k_qgemm<R, C, B, Q, K, N, false, QB, PL>), a.grid, dim3(256), 0, a.st, a.W, a.Ws, a.X, a.Xs,
+                     a.nb, a.nct, a.mpad, a.y, a.ldy, a.m_rows, a.slice_stride, ActEpi{});
+}
+
+// Chunking: 4-block chunks where the quarters are whole chunks; one K slice
+// with quarters inside chunks (QB); every chunk preloaded for 16 x 16 wave
+// tiles over 4..8 chunks (pre4) and for short 1-block-chunk slices (pre);
+// 1-block chunks otherwise.
+template <int R, int C, int B, int Q>
+static void qg_go_tile(const QgLaunch& a) {
+  if constexpr (R == 1 && C == 1) {
+    if (a.pre4) { a.once ? qg_go<R, C, B, Q, 4, true, false, 8>(a) : qg_go<R, C, B, Q, 4, false, false, 8>(a); return; }
+  }
+  if (a.kc4) { a.once ? qg_go<R, C, B, Q, 4, true, false, 0>(a) : qg_go<R, C, B, Q, 4, false, false, 0>(a); return; }
+  if constexpr (Q == 4) {
+    a.once ? qg_go<R, C, B, 4, 4, true, true, 0>(a) : qg_go<R, C, B, 4, 4, false, true, 0>(a);
+  } else {
+    if (a.pre) { a.once ? qg_go<R, C, B, Q, 1, true, false, 8>(a) : qg_go<R, C, B, Q, 1, false, false, 8>(a); return; }
+    a.once ? qg_go<R, C, B, Q, 1, true, false, 0>(a) : qg_go<R, C, B, Q, 1, false, false, 0>(a);
+  }
+}
+
+template <int R, int C, int B>
+static void qg_dispatch_q(const QgLaunch& a, int nq) {
+  if (nq == 4) qg_go_tile<R, C, B, 4>(a);
+  else if (nq == 2) qg_go_tile<R, C, B, 2>(a);
+  else qg_go_tile<R, C, B, 1>(a);
+}
+
+template <int B>
+static void qg_dispatch_t(const QgLaunch& a, const QgPlan& p) {
+  if (p.rt == 4) qg_dispatch_q<4, 1, B>(a, p.nq);
+  else if (p.rt == 2 && p.ct == 1) qg_go_tile<2, 1, B, 1>(a);
+  else if (p.rt == 2) qg_dispatch_q<2, 2, B>(a, p.nq);
+  else if (p.ct == 4) qg_dispatch_q<1, 4, B>(a, p.nq);
+  else if (p.ct == 2) qg_dispatch_q<1, 2, B>(a, p.nq);
+  else qg_dispatch_q<1, 1, B>(a, p.nq);
+}
+
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
                         int ldy, int splits, size_t slice_stride) {
   const int nb = w.k / 32;
@@ -792,57 +848,17 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   const uint32_t* W = (const uint32_t*)w.w;
   const bool kc4 = (nb / 4) % 4 == 0;  // quarters are whole 4-block chunks
   const bool once = grid.z == 1;      // every weight is read by one workgroup
-  const bool pre = !kc4 && (4 / splits) * (nb / 4) <= 8;  // 1-block chunks, all preloaded
-#define RSTR_QG_L(R, C, B, Q, K, N)                                                                     \
-  hipLaunchKernelGGL((k_qgemm<R, C, B, Q, K, N>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
-                     x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
-#define RSTR_QG_LP(R, C, B, Q, N)                                                                              \
-  hipLaunchKernelGGL((k_qgemm<R, C, B, Q, 1, N, false, false, 8>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, \
-                     nct, x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
-#define RSTR_QG(R, C, B, Q)                                        \
-  do {                                                             \
-    if (kc4 && once) RSTR_QG_L(R, C, B, Q, 4, true);               \
-    else if (kc4) RSTR_QG_L(R, C, B, Q, 4, false);                 \
-    else if (pre && once) RSTR_QG_LP(R, C, B, Q, true);            \
-    else if (pre) RSTR_QG_LP(R, C, B, Q, false);                   \
-    else if (once) RSTR_QG_L(R, C, B, Q, 1, true);                 \
-    else RSTR_QG_L(R, C, B, Q, 1, false);                          \
-  } while (0)
-// one K slice: 4-block chunks also where a quarter is not whole chunks (QB)
-#define RSTR_QG_LB(R, C, B, N)                                                                                \
-  hipLaunchKernelGGL((k_qgemm<R, C, B, 4, 4, N, false, true>), grid, dim3(256), 0, st, W, w.s, x.q, x.s, nb, nct, \
-                     x.mpad, y, ldy, m_rows, slice_stride, ActEpi{})
-#define RSTR_QG4(R, C, B)                                          \
-  do {                                                             \
-    if (kc4 && once) RSTR_QG_L(R, C, B, 4, 4, true);               \
-    else if (kc4) RSTR_QG_L(R, C, B, 4, 4, false);                 \
-    else if (once) RSTR_QG_LB(R, C, B, true);                      \
-    else RSTR_QG_LB(R, C, B, false);                               \
-  } while (0)
-#define RSTR_QG_Q(R, C, B)                 \
-  do {                                     \
-    if (p.nq == 4) RSTR_QG4(R, C, B);      \
-    else if (p.nq == 2) RSTR_QG(R, C, B, 2); \
-    else RSTR_QG(R, C, B, 1);              \
-  } while (0)
-#define RSTR_QG_T(B)                                   \
-  do {                                                 \
-    if (p.rt == 4) RSTR_QG_Q(4, 1, B);                 \
-    else if (p.rt == 2 && p.ct == 1) RSTR_QG(2, 1, B, 1); \
-    else if (p.rt == 2) RSTR_QG_Q(2, 2, B);            \
-    else if (p.ct == 4) RSTR_QG_Q(1, 4, B);            \
-    else if (p.ct == 2) RSTR_QG_Q(1, 2, B);            \
-    else RSTR_QG_Q(1, 1, B);                           \
-  } while (0)
-  if (w.bits == 4) RSTR_QG_T(4);
-  else RSTR_QG_T(8);
-#undef RSTR_QG_T
-#undef RSTR_QG_Q
-#undef RSTR_QG4
-#undef RSTR_QG_LB
-#undef RSTR_QG
-#undef RSTR_QG_LP
-#undef RSTR_QG_L
+  // every chunk preloaded: 1-block chunks of short slices; Q4 16-row tiles over
+  // 4..8 4-block chunks below 16384 columns (kernel benchmark, weights from HBM,
+  // one and 16 rows: Llama-3-8B o 7.1 -> 5.7 us, qkv 7.3 -> 7.1; Qwen3 down 5.7 ->
+  // 4.7; Gemma down 4.4 -> 4.0; slower at 2 chunks and for the 28672-wide gate/up;
+  // Q8 doubles the preloaded registers and is left on the chunk loop)
+  const int nchunk4 = (4 / splits) * (nb / 4) / 4;
+  const bool pre = !kc4 && (4 / splits) * (nb / 4) <= 8;
+  const bool pre4 = kc4 && p.rt == 1 && nchunk4 >= 4 && nchunk4 <= 8 && w.n < 16384 && w.bits == 4;
+  QgLaunch L{grid, st, W, w.s, x.q, x.s, nb, nct, x.mpad, y, ldy, m_rows, slice_stride, kc4, once, pre, pre4};
+  if (w.bits == 4) qg_dispatch_t<4>(L, p);
+  else qg_dispatch_t<8>(L, p);
   return hipGetLastError();
 }
 
