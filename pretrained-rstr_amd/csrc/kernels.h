@@ -122,6 +122,24 @@ hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
                              const int32_t* page_table, int32_t* lane_tab, float* part,
                              int max_items);
+// The decode step's per-row qkv post-processing (launch_qkv_post) done by the
+// few-item attention kernel instead of a launch of its own: each item computes
+// its heads' q from the projection slices (qk-norm, RoPE at the row's position),
+// and the item that holds a lane's newest token appends that token's K/V (fp16
+// RNE) before its first page load.  Only valid when no lane's visible range
+// holds another lane's appended slot (attn_fuses_qkv says when the few-item
+// kernel runs; the caller checks the descriptors).
+struct AttnQkv {
+  Slices y;                          // qkv projection output in slices
+  const float *qn, *kn;              // qk-norm gains (null: none)
+  float goff, eps;
+  const float *cos_t, *sin_t;        // [maxpos][hd/2] of the layer's theta
+  const int32_t *positions, *slots, *lengths;
+  uint16_t *kpages, *vpages;         // the layer's slabs (written at the slots)
+};
+bool attn_fuses_qkv(const AttnGeom& g, int max_items);
+hipError_t launch_attn_split_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk,
+                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items);
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                              int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q);

@@ -1916,6 +1916,90 @@ __global__ __launch_bounds__(64) void k_attn_split(
 #undef RSTR_ATTN_READ_Q
 }
 
+// ---- qkv post-processing inside the few-item kernel (AttnQkv) --------------------
+// One head of row `src`'s qkv output with k_qkv_post's arithmetic: lane l <
+// HD/4 holds elements 4l..4l+3 (slices added in the canonical tree), then the
+// optional RMS norm over the head.
+template <int HD>
+__device__ __forceinline__ f4 qkv_head(const AttnQkv& qk, size_t src, const float* gn, int lane) {
+  constexpr int HD4 = HD / 4;
+  const bool have = lane < HD4;
+  const int cc = have ? lane : 0;
+  f4 v;
+  if (qk.y.n == 1) v = sl_get<1>(qk.y, src + 4 * cc);
+  else if (qk.y.n == 2) v = sl_get<2>(qk.y, src + 4 * cc);
+  else v = sl_get<4>(qk.y, src + 4 * cc);
+  if (gn) {
+    const f4 gg = *reinterpret_cast<const f4*>(gn + 4 * cc);
+    float a = 0.0f;
+    if (have) {
+      a = __builtin_fmaf(v[0], v[0], a);
+      a = __builtin_fmaf(v[1], v[1], a);
+      a = __builtin_fmaf(v[2], v[2], a);
+      a = __builtin_fmaf(v[3], v[3], a);
+    }
+    // HD/4 <= 64 chunks: lane l holds slot l alone, and the tree over 64
+    // lanes equals the 256-slot tree (the other slots are +0)
+    const float r = rms_scale(wave_tree_sum(a), HD, qk.eps);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = (v[i] * r) * (qk.goff + gg[i]);
+  }
+  return v;
+}
+
+// The item's q heads (wave w: heads w, w+4, ...) into qst[G][HD], rotated at the
+// row's position; the item holding the lane's newest token also writes that
+// token's K (wave 0: norm, RoPE) and V (wave 1) to the pages at the slot.
+// Every write is complete and visible to the workgroup on return.
+template <int HD, int G>
+__device__ void attn_qkv_prologue(const AttnQkv& qk, const AttnItem& it, int n_kv, int lane, int wave,
+                                  float* qst) {
+  constexpr int HD4 = HD / 4, HALF = HD / 2;
+  const int kvr = n_kv * HD, qd = n_kv * G * HD;
+  const size_t yr = (size_t)it.b * (qd + 2 * kvr);
+  const bool have = lane < HD4;
+  const int slot = uni(qk.slots[it.b]);
+  const bool newest = slot >= 0 && it.t1 == uni(qk.lengths[it.b]);
+  const int pos = uni(qk.positions[it.b]);
+  float* kst = qst + G * HD;
+  for (int h = wave; h < G; h += 4) {
+    const f4 v = qkv_head<HD>(qk, yr + (size_t)(it.kvh * G + h) * HD, qk.qn, lane);
+    if (have) *reinterpret_cast<f4*>(qst + h * HD + 4 * lane) = v;
+  }
+  if (newest && wave == 0) {
+    const f4 v = qkv_head<HD>(qk, yr + qd + (size_t)it.kvh * HD, qk.kn, lane);
+    if (have) *reinterpret_cast<f4*>(kst + 4 * lane) = v;
+  }
+  if (newest && wave == 1) {
+    const f4 v = qkv_head<HD>(qk, yr + qd + kvr + (size_t)it.kvh * HD, nullptr, lane);
+    if (have) {
+      uint16_t* dst = qk.vpages + (size_t)slot * kvr + it.kvh * HD;
+#pragma unroll
+      for (int i = 0; i < 4; i++) dst[4 * lane + i] = f2h_bits(v[i]);
+    }
+  }
+  __syncthreads();
+  // HF rotate-half: y_i = x_i c - x_{i+h} s, y_{i+h} = x_{i+h} c + x_i s
+  const float* ct = qk.cos_t + (size_t)pos * HALF;
+  const float* stt = qk.sin_t + (size_t)pos * HALF;
+  for (int h = wave; h < G; h += 4)
+    for (int i = lane; i < HALF; i += 64) {
+      const float a = qst[h * HD + i], b = qst[h * HD + i + HALF], c = ct[i], sn = stt[i];
+      qst[h * HD + i] = (a * c) - (b * sn);
+      qst[h * HD + i + HALF] = (b * c) + (a * sn);
+    }
+  if (newest && wave == 0) {
+    uint16_t* dst = qk.kpages + (size_t)slot * kvr + it.kvh * HD;
+    for (int i = lane; i < HALF; i += 64) {
+      const float a = kst[i], b = kst[i + HALF], c = ct[i], sn = stt[i];
+      dst[i] = f2h_bits((a * c) - (b * sn));
+      dst[i + HALF] = f2h_bits((b * c) + (a * sn));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K/V stores are complete
+  __syncthreads();                     // rotated q in LDS; the appended row is visible to the DMAs that follow
+}
+
 // ---- few-item attention: one workgroup of four waves per item -------------------
 // The same canonical order as k_attn_split, for launches whose whole work list
 // fits in two rounds of resident workgroups (few lanes, short contexts).  There
@@ -1933,12 +2017,18 @@ __global__ __launch_bounds__(64) void k_attn_split(
 // A ring of RB chunks, each filled by all 256 threads' DMAs, streams the
 // item's K then V chunks and drains between items.  Every list position is
 // static (attn_static_rounds gives one or two rounds here), so no claims.
-template <int HD, int G, int RB>
-__global__ __launch_bounds__(256) void k_attn_split_wg(
+//
+// QKV: the item's query comes from the qkv projection slices through
+// attn_qkv_prologue (q is unused), and the lane's newest K/V row is appended
+// by the item that holds it, so no separate qkv launch precedes this one.
+// (The QKV form keeps three waves per SIMD for G <= 4: a few kernel-constant
+// prologue values then live in scratch and are reloaded once per item.)
+template <int HD, int G, int RB, bool QKV = false>
+__global__ __launch_bounds__(256, QKV && G <= 4 ? 3 : 1) void k_attn_split_wg(
     int n_kv, int page_size, int ps_shift, int pps, float scale,
-    const float* __restrict__ q, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ vp,
+    const float* __restrict__ q, const uint16_t* kp, const uint16_t* vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ n_items,
-    const int4* __restrict__ items, float* __restrict__ part) {
+    const int4* __restrict__ items, float* __restrict__ part, AttnQkv qk) {
   constexpr int NP = HD / 8;       // 16-byte pieces per row
   constexpr int CT = 16;           // tokens per chunk
   constexpr int CU16 = CT * NP;    // 16-byte units per chunk
@@ -1951,7 +2041,8 @@ __global__ __launch_bounds__(256) void k_attn_split_wg(
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   u32x4* ring = reinterpret_cast<u32x4*>(smem);                   // [RB][CU16]
   float* red = reinterpret_cast<float*>(ring + RB * CU16);        // [4][G] wave maxima, then l
-  float* sc = red + 4 * G;                                        // [split][G] scores
+  float* qst = red + 4 * G;                                       // [G + 1][HD] q (and K) staging
+  float* sc = qst + (G + 1) * HD;                                 // [split][G] scores
   float* comb = reinterpret_cast<float*>(smem);                   // [4][G][HD] o, after PV
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2000,7 +2091,18 @@ __global__ __launch_bounds__(256) void k_attn_split_wg(
     };
     // this thread's query pieces: slice j of each head
     float qv[G][NCL][8];
-    {
+    if constexpr (QKV) {
+      attn_qkv_prologue<HD, G>(qk, it, n_kv, lane, wave, qst);
+#pragma unroll
+      for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int i = 0; i < NCL; i++) {
+          const f4 a = *reinterpret_cast<const f4*>(qst + h * HD + 8 * (j + 16 * i));
+          const f4 b4 = *reinterpret_cast<const f4*>(qst + h * HD + 8 * (j + 16 * i) + 4);
+#pragma unroll
+          for (int e = 0; e < 4; e++) { qv[h][i][e] = a[e]; qv[h][i][4 + e] = b4[e]; }
+        }
+    } else {
       const float* qg = q + ((size_t)it.b * (n_kv * G) + it.kvh * G) * HD;
 #pragma unroll
       for (int h = 0; h < G; h++)
@@ -2177,22 +2279,30 @@ struct AttnSplit {
   static constexpr bool kWG = HD == 128 || HD == 256;
   static constexpr int RBW = HD == 128 ? 8 : 4;
   static size_t lds_wg(const AttnGeom& g) {
-    return (size_t)RBW * 16 * (HD / 8) * 16 + sizeof(float) * G * (4 + (size_t)g.split);
+    return (size_t)RBW * 16 * (HD / 8) * 16 + sizeof(float) * (G * (4 + (size_t)g.split) + (G + 1) * HD);
   }
+  template <bool QKV = false>
   static int wg_capacity(const AttnGeom& g) {
     if constexpr (!kWG) {
       return 0;
     } else {
       int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_split_wg<HD, G, RBW>, 256, lds_wg(g)) != hipSuccess)
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_attn_split_wg<HD, G, RBW, QKV>, 256, lds_wg(g)) !=
+          hipSuccess)
         return 0;
       return device_cus() * n;
     }
   }
+  // The QKV form only where the whole work list is one round of resident
+  // workgroups: its per-item prologue (the item's q from the projection
+  // slices) sits on each item's path, so a second round pays it twice.
+  // Measured: one lane of Llama-3-8B 2.43 -> 2.385 ms/step and config1
+  // 0.761 -> 0.753 (one round), config2 0.794 -> 0.802 (two rounds).
+  template <bool QKV = false>
   static bool use_wg(const AttnGeom& g, int max_items) {
     if (!kWG || !pg16(g)) return false;
-    const int cap = wg_capacity(g);
-    return cap > 0 && max_items <= 2 * cap;
+    const int cap = wg_capacity<QKV>(g);
+    return cap > 0 && max_items <= (QKV ? 1 : 2) * cap;
   }
   static int grid(const AttnGeom& g, int max_items) {
     if (use_wg(g, max_items)) return std::max(1, std::min(wg_capacity(g), max_items));
@@ -2211,12 +2321,29 @@ struct AttnSplit {
     if constexpr (kWG) {
       if (use_wg(g, max_items)) {
         hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv, g.page_size,
-                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part);
+                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{});
         return;
       }
     }
     hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
                        kp, vp, pt, n_items, items, ctr, part);
+  }
+  // the few-item kernel with the qkv post-processing in its prologue
+  static bool launch_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk, const int32_t* pt, int32_t* tab,
+                         float* part, int max_items) {
+    if constexpr (kWG) {
+      if (!use_wg<true>(g, max_items)) return false;
+      const int R = std::max(1, std::min(wg_capacity<true>(g), max_items));
+      const int32_t* n_items = tab + 4 * g.batch;
+      const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch));
+      const int shift = __builtin_ctz((unsigned)g.page_size);
+      hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
+                         g.page_size, shift, g.pps, g.scale, nullptr, qk.kpages, qk.vpages, pt, n_items, items,
+                         part, qk);
+      return true;
+    } else {
+      return false;
+    }
   }
 };
 
@@ -2262,6 +2389,28 @@ hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
   }
   RSTR_ATTN_DISPATCH(g, RSTR_AL);
 #undef RSTR_AL
+  return hipErrorInvalidValue;
+}
+
+bool attn_fuses_qkv(const AttnGeom& g, int max_items) {
+#define RSTR_AF(HD_, G_, L_)                                                                 \
+  return AttnSplit<HD_, G_, L_>::use_wg(g, max_items) && AttnSplit<HD_, G_, L_>::template use_wg<true>(g, max_items)
+  RSTR_ATTN_DISPATCH(g, RSTR_AF);
+#undef RSTR_AF
+  return false;
+}
+
+hipError_t launch_attn_split_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk,
+                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items) {
+  if (g.hd > 256 || g.hd % 4) return hipErrorInvalidValue;
+#define RSTR_AQ(HD_, G_, L_)                                                                                 \
+  {                                                                                                         \
+    if (!AttnSplit<HD_, G_, L_>::launch_qkv(st, g, qk, page_table, lane_tab, part, max_items))               \
+      return hipErrorInvalidValue;                                                                          \
+    return hipGetLastError();                                                                               \
+  }
+  RSTR_ATTN_DISPATCH(g, RSTR_AQ);
+#undef RSTR_AQ
   return hipErrorInvalidValue;
 }
 

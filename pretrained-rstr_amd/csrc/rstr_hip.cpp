@@ -142,6 +142,7 @@ struct StagedDev {                        // one uploaded schedule step
   int32_t n_cow;
   int64_t prime_off;
   int32_t n_prime;
+  bool fused;                             // qkv post-processing inside attention (see rstr_decoder)
 };
 
 struct rstr_decoder {
@@ -157,6 +158,11 @@ struct rstr_decoder {
   ActBuf act;
   ActBuf act_ff;                                    // down-projection input when gate/up fuses the activation
   bool fuse_act = false;
+  // qkv post-processing (qk-norm, RoPE, K/V append) inside the few-item
+  // attention kernel, for steps where no lane's visible range holds another
+  // lane's appended slot (`mark`: scratch of that check, one word per page)
+  bool fuse_qkv = false;
+  std::vector<int32_t> mark;
   int32_t* desc = nullptr;                          // device descriptors
   int32_t* lane_tab = nullptr;                      // [2][tabw] attention work tables
   size_t tabw = 0;                                  // words per work table
@@ -985,6 +991,8 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   d->tabw = attn_tab_words(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps, split, 0,
                                      md.attn_scale}, d->max_items);
   if (d->tabw == 0 && e == hipSuccess) e = hipErrorInvalidValue;
+  d->fuse_qkv = head_tail && d->tabw && attn_fuses_qkv(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps,
+                                                                split, 0, md.attn_scale}, d->max_items);
   A(dmalloc(&d->lane_tab, 2 * d->tabw));
   A(dmalloc(&d->tokbuf, (size_t)batch));
   A(dmalloc(&d->amax_cand, (size_t)2 * batch * argmax_segments(batch, md.vocab)));
@@ -1123,8 +1131,40 @@ extern "C" int rstr_decode_logits(rstr_decoder* d, float* out) {
 // Validation of one step's descriptors (the checks Raster's
 // attention/validate-routing! and validate-query-values! make, plus the
 // decode invariant that the appended row is the route's last visible token).
+// True when no lane's visible range holds another lane's append slot, i.e.
+// each lane's new K/V row is read only by that lane in this step (what the
+// page pool's copy-on-write guarantees for decode; bulk-prefill tiles are the
+// opposite case).  Run on validated descriptors.
+static bool appends_private(rstr_decoder* d, const int32_t* slots, const int32_t* pt, const int32_t* len) {
+  const int ps = d->p->page_size;
+  auto& mk = d->mark;
+  if ((int64_t)mk.size() != (int64_t)d->p->physical_pages) mk.assign(d->p->physical_pages, -1);
+  bool ok = true;
+  for (int b = 0; b < d->B; b++) {
+    if (slots[b] < 0) continue;
+    const int32_t P = slots[b] / ps;
+    if (mk[P] != -1) ok = false;  // two appends in one page
+    mk[P] = b;
+  }
+  for (int c = 0; ok && c < d->B; c++) {
+    const int32_t L = len[c];
+    const int32_t* row = pt + (int64_t)c * d->pps;
+    for (int32_t i = 0; i < (L + ps - 1) / ps; i++) {
+      const int32_t b = mk[row[i]];
+      if (b >= 0 && b != c && (int64_t)i * ps + slots[b] % ps < L) {
+        ok = false;
+        break;
+      }
+    }
+  }
+  for (int b = 0; b < d->B; b++)
+    if (slots[b] >= 0) mk[slots[b] / ps] = -1;
+  return ok;
+}
+
 static int validate_step(rstr_decoder* d, const int32_t* slots, const int32_t* rows, const int32_t* pos,
-                         const int32_t* pt, const int32_t* len, const int32_t* start) {
+                         const int32_t* pt, const int32_t* len, const int32_t* start, bool* fused = nullptr) {
+  if (fused) *fused = false;
   rstr_session* s = d->m->s;
   if (!slots || !rows || !pos || !pt || !len || !start) return fail(s, RSTR_E_INVALID, "null descriptor");
   int ps = d->p->page_size;
@@ -1157,6 +1197,7 @@ static int validate_step(rstr_decoder* d, const int32_t* slots, const int32_t* r
       if (want != slots[b]) return fail(s, RSTR_E_INVALID, "append slot is not the route's last token");
     }
   }
+  if (fused) *fused = d->fuse_qkv && appends_private(d, slots, pt, len);
   return RSTR_OK;
 }
 
@@ -1188,7 +1229,7 @@ struct Prof {
 
 // Enqueue the whole decode step on `st`; every kernel reads descriptors from
 // device memory so the sequence can be captured once and replayed.
-static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
+static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool fused) {
   const auto& md = d->m->d;
   const int B = d->B, dm = md.d_model, hd = md.head_dim;
   const float goff = md.gain_offset ? 1.0f : 0.0f;
@@ -1235,14 +1276,24 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
     uint16_t* vp = d->p->slabs[L + l];
     const size_t sq = (size_t)B * d->nqkv, sd = (size_t)B * dm, sg = (size_t)B * 2 * md.d_ff;
     run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.qkv, d->act, B, d->yqkv, d->nqkv, d->s_qkv, sq); });
-    run(RSTR_K_QKV_POST, [&] {
-      return launch_qkv_post(st, Slices{d->yqkv, d->s_qkv, sq}, B, md.n_q, md.n_kv, hd, W.q_norm, W.k_norm, goff, md.eps,
-                             d->rope_cos + (size_t)ti * d->maxpos * half,
-                             d->rope_sin + (size_t)ti * d->maxpos * half, pos, slots, d->qr, kp, vp);
-    });
-    run(RSTR_K_ATTN_SPLIT, [&] {
-      return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
-    });
+    const float* cos_l = d->rope_cos + (size_t)ti * d->maxpos * half;
+    const float* sin_l = d->rope_sin + (size_t)ti * d->maxpos * half;
+    if (fused) {
+      // qk-norm, RoPE and the K/V append in the few-item attention kernel's prologue
+      run(RSTR_K_ATTN_SPLIT, [&] {
+        const AttnQkv qk{Slices{d->yqkv, d->s_qkv, sq}, W.q_norm, W.k_norm, goff, md.eps, cos_l, sin_l, pos, slots,
+                         len, kp, vp};
+        return launch_attn_split_qkv(st, geo[wi], qk, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
+      });
+    } else {
+      run(RSTR_K_QKV_POST, [&] {
+        return launch_qkv_post(st, Slices{d->yqkv, d->s_qkv, sq}, B, md.n_q, md.n_kv, hd, W.q_norm, W.k_norm, goff,
+                               md.eps, cos_l, sin_l, pos, slots, d->qr, kp, vp);
+      });
+      run(RSTR_K_ATTN_SPLIT, [&] {
+        return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
+      });
+    }
     run(RSTR_K_ATTN_MERGE, [&] {
       return launch_attn_merge(st, geo[wi], len, d->lane_tab + wi * tabw, d->part, nullptr, &d->act);
     });
@@ -1277,13 +1328,15 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof) {
   return e;
 }
 
-static int run_step_device(rstr_decoder* d) {
+// The step graph is captured in the decoder's own form (fused qkv when
+// fuse_qkv); a step that cannot take that form runs eagerly.
+static int run_step_device(rstr_decoder* d, bool fused) {
   rstr_session* s = d->m->s;
-  if (d->use_graph) {
+  if (d->use_graph && fused == d->fuse_qkv) {
     if (!d->graph) {
       hipGraph_t g = nullptr;
       HIPCHK(s, hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
-      hipError_t e = enqueue_step(d, s->stream, nullptr);
+      hipError_t e = enqueue_step(d, s->stream, nullptr, d->fuse_qkv);
       hipError_t e2 = hipStreamEndCapture(s->stream, &g);
       if (e != hipSuccess || e2 != hipSuccess) {
         if (g) hipGraphDestroy(g);
@@ -1296,7 +1349,7 @@ static int run_step_device(rstr_decoder* d) {
     }
     HIPCHK(s, hipGraphLaunch(d->graph, s->stream));
   } else {
-    HIPCHK(s, enqueue_step(d, s->stream, nullptr));
+    HIPCHK(s, enqueue_step(d, s->stream, nullptr, fused));
   }
   d->has_logits = d->head_tail;
   return RSTR_OK;
@@ -1308,7 +1361,8 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
   if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
   rstr_session* s = d->m->s;
   if (!d->head_tail) return fail(s, RSTR_E_STATE, "a bulk-prefill decoder has no head; use rstr_prefill_range");
-  int rc = validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions);
+  bool fused = false;
+  int rc = validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions, &fused);
   if (rc) return rc;
   if (!tokens_out) return fail(s, RSTR_E_INVALID, "null token output");
   HIPCHK(s, hipSetDevice(s->device));
@@ -1316,7 +1370,7 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
   pack_desc(d, d->h_desc, slots, row_offsets, positions, page_table, lengths, start_positions);
   HIPCHK(s, hipMemcpyAsync(d->desc, d->h_desc, sizeof(int32_t) * d->desc_words, hipMemcpyHostToDevice,
                            s->stream));
-  if ((rc = run_step_device(d))) return rc;
+  if ((rc = run_step_device(d, fused))) return rc;
   HIPCHK(s, hipMemcpyAsync(d->h_tok, d->tokbuf, sizeof(int32_t) * d->B, hipMemcpyDeviceToHost, s->stream));
   HIPCHK(s, hipStreamSynchronize(s->stream));
   std::memcpy(tokens_out, d->h_tok, sizeof(int32_t) * d->B);
@@ -1354,7 +1408,7 @@ extern "C" int rstr_prefill_range(rstr_decoder* d, const int32_t* tokens, const 
   pack_desc(d, d->h_desc, slots, rows.data(), positions, pt.data(), len.data(), start.data());
   HIPCHK(s, hipMemcpyAsync(d->desc, d->h_desc, sizeof(int32_t) * d->desc_words, hipMemcpyHostToDevice,
                            s->stream));
-  if ((rc = run_step_device(d))) return rc;
+  if ((rc = run_step_device(d, false))) return rc;
   HIPCHK(s, hipStreamSynchronize(s->stream));
   return RSTR_OK;
 }
@@ -1370,10 +1424,11 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
   int64_t words = 0, pages = 0;
   uint64_t fill_seed = 0;
   bool fill_seed_set = false;
+  std::unique_ptr<bool[]> fused_steps(new bool[n]());
   for (int32_t i = 0; i < n; i++) {
     const auto& t = steps[i];
     int rc = validate_step(d, t.slots, t.row_offsets, t.positions, t.page_table, t.lengths,
-                           t.start_positions);
+                           t.start_positions, &fused_steps[i]);
     if (rc) return rc;
     if (t.n_fill < 0 || t.n_cow < 0 || (t.n_fill && !t.fill_pages) || (t.n_cow && !t.cow_pairs))
       return fail(s, RSTR_E_INVALID, "invalid staged fill or copy list");
@@ -1440,6 +1495,7 @@ extern "C" int rstr_schedule_upload(rstr_decoder* d, const rstr_staged_step* ste
     po += 2 * t.n_cow;
     sd.prime_off = po;
     sd.n_prime = t.n_prime;
+    sd.fused = fused_steps[i];
     std::memcpy(hpages.data() + po, t.prime_lanes, sizeof(int32_t) * t.n_prime);
     std::memcpy(hpages.data() + po + t.n_prime, t.prime_tokens, sizeof(int32_t) * t.n_prime);
     po += 2 * t.n_prime;
@@ -1487,7 +1543,7 @@ extern "C" int rstr_schedule_run(rstr_decoder* d, int32_t first, int32_t count, 
   HIPCHK(s, hipEventRecord(a, s->stream));
   for (int32_t i = first; i < first + count; i++) {
     HIPCHK(s, enqueue_staged_prelude(d, d->sched[i], s->stream));
-    if ((rc = run_step_device(d))) return rc;
+    if ((rc = run_step_device(d, d->sched[i].fused))) return rc;
     HIPCHK(s, hipMemcpyAsync(d->sched_tok + (size_t)i * d->B, d->tokbuf, sizeof(int32_t) * d->B,
                              hipMemcpyDeviceToDevice, s->stream));
   }
@@ -1517,7 +1573,7 @@ extern "C" int rstr_decoder_profile_steps(rstr_decoder* d, int32_t first, int32_
   for (int32_t i = first; i < first + count; i++) {
     Prof prof;
     HIPCHK(s, enqueue_staged_prelude(d, d->sched[i], s->stream));
-    HIPCHK(s, enqueue_step(d, s->stream, &prof));
+    HIPCHK(s, enqueue_step(d, s->stream, &prof, d->sched[i].fused));
     HIPCHK(s, hipStreamSynchronize(s->stream));
     for (auto& mk : prof.marks) {
       float ms = 0.0f;

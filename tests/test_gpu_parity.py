@@ -499,6 +499,67 @@ def test_fused_gate_up_activation_bit_exact(sess, name, d_model, bits, B):
         _close(r)
 
 
+@pytest.mark.parametrize("name", ["tiny_gemma", "tiny_qwen"])
+def test_lanes_that_read_each_others_appends(sess, name):
+    """Small batches run the qkv post-processing inside the few-item attention
+    kernel, where each lane appends its own new K/V row.  A step whose lanes read
+    each other's new rows (three causal lanes over one route, as a prefill tile
+    lays them out) must still see every append, as the oracle's append-then-attend
+    order does: the decoder runs such a step with the separate qkv launch.  Later
+    steps on private routes return to the fused form."""
+    print(f"case shared appends {name}", flush=True)
+    cfg = configs.MODELS[name]
+    B, ps, pages, pps, maxpos, split = 3, 16, 12, 6, 96, 16
+    start_len = 37
+    pt = np.full((B, pps), -1, np.int32)
+    route = np.array([7, 2, 9, 4], np.int32)
+    for b in range(B):
+        pt[b, :4] = route
+    m = hip.Model(sess, cfg, seed=4)
+    p = hip.Pool(m, ps, pages)
+    d = hip.Decoder(m, p, B, pps, maxpos, split)
+    om = O.Model(cfg, seed=4)
+    od = O.Decoder(om, B, ps, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        for pg in route[:3]:
+            p.fill_synthetic([int(pg)], 23)
+            od.fill_synthetic(int(pg), 23)
+        toks = np.array([11, 12, 13], np.int32)
+        d.prime_lanes(np.arange(B), toks)
+        od.prime_lanes(np.arange(B), toks)
+        # causal step: lane b's new token sits at position start_len + b and lane
+        # b reads positions 0..start_len + b, i.e. the new rows of lanes < b
+        lengths = np.array([start_len + b + 1 for b in range(B)], np.int32)
+        pos = lengths - 1
+        slots = np.array([route[t // ps] * ps + t % ps for t in pos], np.int32)
+        desc = dict(slots=slots, row_offsets=np.arange(B + 1, dtype=np.int32), positions=pos.astype(np.int32),
+                    page_table=pt, lengths=lengths, start_positions=np.zeros(B, np.int32))
+        g = d.step_lanes(**desc)
+        o = od.step_lanes(**desc)
+        assert np.array_equal(g, o)
+        assert np.array_equal(d.logits(), od.logits())
+        for layer in range(cfg["n_layers"]):
+            for slab in (0, 1):
+                assert np.array_equal(p.pages(slab, layer).view(np.uint16), od.slab(slab, layer).view(np.uint16))
+        # then one lane alone on its route (private append): the fused form
+        lengths2 = np.array([start_len + 4, 0, 0], np.int32)
+        t = int(lengths2[0]) - 1
+        slots2 = np.array([route[t // ps] * ps + t % ps, -1, -1], np.int32)
+        desc2 = dict(slots=slots2, row_offsets=np.arange(B + 1, dtype=np.int32),
+                     positions=np.array([t, 0, 0], np.int32), page_table=pt, lengths=lengths2,
+                     start_positions=np.zeros(B, np.int32))
+        d.prime_lanes([0], [5])
+        od.prime_lanes([0], [5])
+        assert d.step_lanes(**desc2)[0] == od.step_lanes(**desc2)[0]
+        assert np.array_equal(d.logits()[0], od.logits()[0])
+    finally:
+        d.close()
+        p.close()
+        m.close()
+        od.close()
+        om.close()
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_one_lane_long_k_weight_streaming(sess, bits):
     """One lane at Llama-3-8B width (first layer, full vocabulary): the MLP down
