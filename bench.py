@@ -528,7 +528,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--live-steps", type=int, default=20, help="steps of the live serving loop (0: skip)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="config5 only: skip the config5_1lane, config2 and config1 sub-runs of the default line")
+                    help="config5 only: skip the config5_1lane, config2, config3, config1 and config4 sub-runs "
+                         "of the default line")
     args = ap.parse_args()
     if args.split is None:
         args.split = SPLITS[args.workload]
@@ -555,11 +556,11 @@ def main():
         # the latency end of the lane range and the small-model config, measured in the
         # same run (the driver records one line): config5's model on one lane, and config2
         out["other_workloads"] = {}
-        for extra, steps in (("config5_1lane", 100), ("config2", 200)):
+        for extra, steps in (("config5_1lane", 100), ("config2", 200), ("config3", 40)):
             sub = argparse.Namespace(**vars(args))
             sub.workload, sub.split, sub.steps, sub.warmup = extra, SPLITS[extra], steps, 10
             sub.live_steps = min(args.live_steps, 10)
-            sub.no_cpu_baseline = args.no_cpu_baseline or extra == "config5_1lane"
+            sub.no_cpu_baseline = args.no_cpu_baseline or extra in ("config5_1lane", "config3")
             sub.cpu_seconds = min(args.cpu_seconds, 6.0)
             r = decode_workload(sub)
             if extra == "config5_1lane" and "cpu_baseline" in out:
@@ -574,6 +575,12 @@ def main():
         r = config1_workload(sub)
         out["other_workloads"]["config1"] = {k: r[k] for k in (
             "value", "unit", "ms_per_step", "steps", "config", "roofline", "cpu_baseline") if k in r}
+        sub = argparse.Namespace(**vars(args))
+        sub.workload, sub.split, sub.steps, sub.warmup = "config4", SPLITS["config4"], 20, 3
+        sub.no_cpu_baseline = True
+        r = attention_workload(sub)
+        out["other_workloads"]["config4"] = {k: r[k] for k in (
+            "metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms") if k in r}
     print(json.dumps(out), flush=True)
 
 
