@@ -58,6 +58,14 @@ def attention_workload(args) -> dict:
     every lane's full pages drawn from one shared run of pages (a common prefix),
     so 25% of full pages are shared across lanes.  Reports logical and unique KV
     GB/s of the split kernel (merge timed beside it)."""
+    sess = hip.Session(0)
+    try:
+        return _attention_workload(args, sess)
+    finally:
+        sess.close()  # also closes the model, pool and decoders on an error
+
+
+def _attention_workload(args, sess) -> dict:
     name, B, seed = ATTN_WORKLOADS[args.workload]
     cfg = dict(configs.MODELS[name], n_layers=1)
     ps, n_kv, hd, n_q = 16, cfg["n_kv"], cfg["head_dim"], cfg["n_q"]
@@ -66,7 +74,6 @@ def attention_workload(args) -> dict:
     logical = int(lengths.sum()) * row_bytes
     unique_tokens = int(shared_n.max()) * ps + int((lengths - shared_n * ps).sum())
     unique = unique_tokens * row_bytes
-    sess = hip.Session(0)
     model = hip.Model(sess, cfg, seed=1)
     pool = hip.Pool(model, ps, physical)
     pool.fill_synthetic(np.arange(physical, dtype=np.int32), seed)
@@ -120,6 +127,14 @@ def config1_workload(args) -> dict:
     runs the same prompt with f32 K/V (decoder.clj:304-310) on all host cores,
     reported beside the host's STREAM-triad bandwidth, since one token streams
     every packed weight from host DRAM."""
+    sess = hip.Session(0)
+    try:
+        return _config1_workload(args, sess)
+    finally:
+        sess.close()  # also closes the model, pool and decoders on an error
+
+
+def _config1_workload(args, sess) -> dict:
     name, bits, P, G, seed = CPU_WORKLOADS[args.workload]
     cfg = configs.with_bits(configs.MODELS[name], bits)
     ps, maxpos, split = 16, P + G, args.split
@@ -148,7 +163,6 @@ def config1_workload(args) -> dict:
                 times.append(dt)
         return out, times
 
-    sess = hip.Session(0)
     model = hip.Model(sess, cfg, seed=1)
     pool = hip.Pool(model, ps, pps)
     dec = hip.Decoder(model, pool, 1, pps, maxpos, split)
@@ -553,44 +567,57 @@ def main():
         return
     out = decode_workload(args)
     if args.workload == "config5" and not args.no_extra:
-        # the latency end of the lane range and the small-model config, measured in the
-        # same run (the driver records one line): config5's model on one lane, and config2
+        # the other BASELINE configurations, measured in the same run (the driver
+        # records one line); a sub-run that fails records its error and leaves the
+        # config5 measurement intact
         out["other_workloads"] = {}
-        for extra, steps in (("config5_1lane", 100), ("config2", 200), ("config3", 40)):
+
+        def sub_run(name, fn, keys, **over):
             sub = argparse.Namespace(**vars(args))
-            sub.workload, sub.split, sub.steps, sub.warmup = extra, SPLITS[extra], steps, 10
-            sub.live_steps = min(args.live_steps, 10)
-            sub.no_cpu_baseline = args.no_cpu_baseline or extra in ("config5_1lane", "config3")
-            sub.cpu_seconds = min(args.cpu_seconds, 6.0)
-            r = decode_workload(sub)
-            if extra == "config5_1lane" and "cpu_baseline" in out:
+            sub.workload, sub.split = name, SPLITS[name]
+            for k, v in over.items():
+                setattr(sub, k, v)
+            try:
+                r = fn(sub)
+            except Exception as e:  # keep the headline line
+                log(f"{name} sub-run failed: {e!r}")
+                out["other_workloads"][name] = {"error": repr(e)}
+                return
+            if name == "config5_1lane" and "cpu_baseline" in out:
                 # the oracle's one-lane Llama-3-8B decode is this workload's CPU baseline too
                 r["cpu_baseline"] = dict(out["cpu_baseline"], sample="the config5 line's: "
                                          + out["cpu_baseline"].get("sample", ""))
-            out["other_workloads"][extra] = {k: r[k] for k in (
-                "value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline", "step_roofline",
-                "kernel_ms_per_step", "kernel_classes", "live_loop", "cpu_baseline") if k in r}
-        sub = argparse.Namespace(**vars(args))
-        sub.workload, sub.warmup, sub.split = "config1", 1, SPLITS["config1"]
-        r = config1_workload(sub)
-        out["other_workloads"]["config1"] = {k: r[k] for k in (
-            "value", "unit", "ms_per_step", "steps", "config", "roofline", "cpu_baseline") if k in r}
-        sub = argparse.Namespace(**vars(args))
-        sub.workload, sub.split, sub.steps, sub.warmup = "config4", SPLITS["config4"], 20, 3
-        sub.no_cpu_baseline = True
-        r = attention_workload(sub)
-        out["other_workloads"]["config4"] = {k: r[k] for k in (
-            "metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms") if k in r}
+            out["other_workloads"][name] = {k: r[k] for k in keys if k in r}
+
+        decode_keys = ("value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline", "step_roofline",
+                       "kernel_ms_per_step", "kernel_classes", "live_loop", "cpu_baseline")
+        for extra, steps in (("config5_1lane", 100), ("config2", 200), ("config3", 40)):
+            sub_run(extra, decode_workload, decode_keys, steps=steps, warmup=10,
+                    live_steps=min(args.live_steps, 10),
+                    no_cpu_baseline=args.no_cpu_baseline or extra in ("config5_1lane", "config3"),
+                    cpu_seconds=min(args.cpu_seconds, 6.0))
+        sub_run("config1", config1_workload,
+                ("value", "unit", "ms_per_step", "steps", "config", "roofline", "cpu_baseline"), warmup=1)
+        sub_run("config4", attention_workload,
+                ("metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms"),
+                steps=20, warmup=3, no_cpu_baseline=True)
     print(json.dumps(out), flush=True)
 
 
 def decode_workload(args) -> dict:
     """One continuous-decode workload of WORKLOADS: plan on the host, replay the
     device-resident schedule in the timed region, profile, live loop, CPU baseline."""
+    sess = hip.Session(0)
+    try:
+        return _decode_workload(args, sess)
+    finally:
+        sess.close()  # also closes the model, pool and decoders on an error
+
+
+def _decode_workload(args, sess) -> dict:
     name, lanes, ps, maxpos, prompt, output, arrivals, seed = WORKLOADS[args.workload]
     cfg = configs.MODELS[name]
     pps = -(-maxpos // ps)
-    sess = hip.Session(0)
     t0 = time.perf_counter()
     model = hip.Model(sess, cfg, seed=1)
     log(f"model bound in {time.perf_counter() - t0:.1f}s, weights {model.weight_bytes / 1e9:.2f} GB")
