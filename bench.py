@@ -232,12 +232,19 @@ def prefill_workload(args) -> dict:
     permuted pages, ``T`` rows per tile through ``rstr_prefill_range`` (layers only).
     Each tile's rows are causal lanes: projections run as one M = T MFMA tile per
     linear, attention reads the route's pages up to each row."""
+    sess = hip.Session(0)
+    try:
+        return _prefill_workload(args, sess)
+    finally:
+        sess.close()  # also closes the model, pool and decoders on an error
+
+
+def _prefill_workload(args, sess) -> dict:
     name, T, P, seed = PREFILL_WORKLOADS[args.workload]
     cfg = configs.MODELS[name]
     ps = 16
     pps = P // ps
     rng = np.random.default_rng(seed)
-    sess = hip.Session(0)
     model = hip.Model(sess, cfg, seed=1)
     physical = 4 * pps
     pool = hip.Pool(model, ps, physical)
@@ -304,11 +311,18 @@ def chunk_workload(args) -> dict:
     (page list copy + gather kernel + device-to-host DMA into pinned memory);
     the roofline is the gather kernel alone (HBM: the payload read from pages
     and written to staging)."""
+    sess = hip.Session(0)
+    try:
+        return _chunk_workload(args, sess)
+    finally:
+        sess.close()  # also closes the model, pool and decoders on an error
+
+
+def _chunk_workload(args, sess) -> dict:
     name, T, npages, seed = CHUNK_WORKLOADS[args.workload]
     cfg = configs.MODELS[name]
     ps = 16
     rng = np.random.default_rng(seed)
-    sess = hip.Session(0)
     model = hip.Model(sess, cfg, seed=1)
     physical = 4 * npages
     pool = hip.Pool(model, ps, physical)
@@ -542,8 +556,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--live-steps", type=int, default=20, help="steps of the live serving loop (0: skip)")
     ap.add_argument("--no-extra", action="store_true",
-                    help="config5 only: skip the config5_1lane, config2, config3, config1 and config4 sub-runs "
-                         "of the default line")
+                    help="config5 only: skip the config5_1lane, config2, config3, config1, config4 and prefill5 "
+                         "sub-runs of the default line")
     args = ap.parse_args()
     if args.split is None:
         args.split = SPLITS[args.workload]
@@ -601,6 +615,10 @@ def main():
         sub_run("config4", attention_workload,
                 ("metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms"),
                 steps=20, warmup=3, no_cpu_baseline=True)
+        # the bulk prefill tile beside the step (chunk5 keeps its own line: its host-link
+        # rate after the runs above reads ~30 GB/s against ~56 GB/s in a fresh process)
+        sub_run("prefill5", prefill_workload, ("metric", "value", "unit", "ms_per_step", "config", "roofline"),
+                steps=2, warmup=1, no_cpu_baseline=True)
     print(json.dumps(out), flush=True)
 
 
