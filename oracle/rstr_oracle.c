@@ -884,7 +884,9 @@ int32_t orc_step_lanes(orc_decoder* d, const int32_t* slots, const int32_t* row_
   int32_t qd = nq * hd, kvr = nkv * hd, ff = D->d_ff;
   float goff = D->gain_offset ? 1.0f : 0.0f;
   float* x = (float*)malloc(sizeof(float) * (size_t)B * dm);
-  float* h = (float*)malloc(sizeof(float) * (size_t)B * dm);
+  /* h also holds the rotated k rows, which are wider than d_model when */
+  /* n_kv * head_dim > d_model */
+  float* h = (float*)malloc(sizeof(float) * (size_t)B * (size_t)(dm > kvr ? dm : kvr));
   float* q = (float*)malloc(sizeof(float) * (size_t)B * qd);
   float* k = (float*)malloc(sizeof(float) * (size_t)B * kvr);
   float* v = (float*)malloc(sizeof(float) * (size_t)B * kvr);

@@ -499,6 +499,30 @@ def test_fused_gate_up_activation_bit_exact(sess, name, d_model, bits, B):
         _close(r)
 
 
+@pytest.mark.parametrize("n_q,n_kv,hd", [(8, 1, 128), (2, 2, 128), (8, 1, 256), (4, 4, 256)])
+def test_few_item_attention_with_qkv_prologue_group_sizes(sess, n_q, n_kv, hd):
+    """Small batches run qk-norm, RoPE and the K/V append inside the few-item
+    attention kernel; its prologue maps query heads to waves (head h on wave
+    h mod 4), so GQA groups of 8 and of 1 take other paths than the shipped
+    configs' groups of 2 and 4.  Decode steps with qk-norm (Qwen flags) and
+    sandwich/GeLU flags (Gemma) equal the oracle bit for bit."""
+    print(f"case qkv prologue n_q={n_q} n_kv={n_kv} hd={hd}", flush=True)
+    base = "tiny_qwen" if hd == 128 else "tiny_gemma"
+    cfg = _cfg(base, n_q=n_q, n_kv=n_kv, head_dim=hd, attn_scale=1.0 / math.sqrt(hd))
+    B = 5
+    prefix = [0, 21, 44, 3, 60]
+    sched = [[0, 1, 2, 3, 4], [1, 2, 4], [0, 1, 2, 3, 4]]
+    r = _run_lanes(sess, cfg, B, prefix, sched, pages=60, pps=10, maxpos=160)
+    try:
+        assert np.array_equal(r["d"].rows(), r["od"].r0())
+        for layer in range(cfg["n_layers"]):
+            for slab in (0, 1):
+                assert np.array_equal(r["p"].pages(slab, layer).view(np.uint16),
+                                      r["od"].slab(slab, layer).view(np.uint16)), (layer, slab)
+    finally:
+        _close(r)
+
+
 @pytest.mark.parametrize("name", ["tiny_gemma", "tiny_qwen"])
 def test_lanes_that_read_each_others_appends(sess, name):
     """Small batches run the qkv post-processing inside the few-item attention
