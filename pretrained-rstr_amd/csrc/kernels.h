@@ -62,8 +62,13 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 bool qgemm_act_fused(int ff, int mpad);
 hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, int ff, int geglu,
                             ActBuf& out);
+// Few-row weight-streaming GEMVs (m_rows <= 4; launch_qgemm picks them per
+// shape): one wave per (column tile, split), or one workgroup per (column
+// tile, split) whose waves share the split's 4-block groups.
 hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
                         int splits, size_t slice_stride);
+hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                           int splits, size_t slice_stride);
 
 // row kernels
 hipError_t launch_rms_quant(hipStream_t st, const float* x, const float* g, float goff, float eps,

@@ -733,6 +733,193 @@ hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   return hipGetLastError();
 }
 
+// Workgroup form of the GEMV: one workgroup per (column tile, split) whose four
+// waves take the split's 4-block groups round robin (wave w: groups w, w+4, ...),
+// so up to 4*GD groups of one column tile are in flight at once; block dots and
+// scales meet in LDS, and the quarter chains run one wave per quarter before
+// wave 0 adds them in the canonical tree.  Same arithmetic as k_qgemv.
+template <int M, int BITS, int NQ, int GD>
+__global__ __launch_bounds__(256) void k_qgemv_wg(const uint32_t* __restrict__ W, const uint16_t* __restrict__ Ws,
+                                                 const _Float16* __restrict__ X, const float* __restrict__ Xs,
+                                                 int nb, int mpad, float* __restrict__ Y, int ldy, int m_rows,
+                                                 size_t slice_stride) {
+  constexpr int DW = BITS == 4 ? 1 : 2;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nn = lane >> 2, bb = lane & 3;
+  const int ct = blockIdx.x, split = blockIdx.y;
+  const int nb4 = nb >> 2, qs = nb >> 2;
+  const int b_begin = split * NQ * qs, nblk = NQ * qs, b_end = b_begin + nblk;
+  const int bq_lo = b_begin >> 2, bq_hi = (b_end - 1) >> 2;
+  const int npair = nblk * M;
+  u32x4* xq = reinterpret_cast<u32x4*>(smem);                      // [pair][2] (8 words)
+  int* xsum = reinterpret_cast<int*>(xq + 2 * npair);              // [pair]
+  float* dsc = reinterpret_cast<float*>(xsum + npair);             // [pair]
+  float* tt = dsc + npair;                                         // [block][M][16]
+  float* dws = tt + (size_t)nblk * M * 16;                         // [block][16]
+  float* pq = dws + (size_t)nblk * 16;                             // [quarter][M][16]
+
+  const uint32_t* wbase = W + (size_t)ct * nb4 * 256 * DW;
+  const uint16_t* sbase = Ws + (size_t)ct * nb4 * 64 + (nn >> 2) * 16 + bb * 4 + (nn & 3);
+  uint32_t wr[GD][4 * DW];
+  uint16_t sr[GD];
+  auto load = [&](int j, int bq) {
+    bq = min(bq, bq_hi);
+    const uint32_t* wp = wbase + (size_t)bq * 256 * DW;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      if constexpr (DW == 1) {
+        wr[j][g] = ld_stream(wp + g * 64 + lane);
+      } else {
+        const u32x2 v = ld_stream(reinterpret_cast<const u32x2*>(wp + (g * 64 + lane) * 2));
+        wr[j][2 * g] = v[0];
+        wr[j][2 * g + 1] = v[1];
+      }
+    }
+    sr[j] = ld_stream(sbase + (size_t)bq * 64);
+  };
+#pragma unroll
+  for (int j = 0; j < GD; j++) load(j, bq_lo + wave + 4 * j);
+
+  // 1. activation rows -> int8 words (as k_qgemv)
+  for (int p0 = 0; p0 < npair * 4; p0 += 256) {
+    const int p = p0 + tid;
+    const int pc = min(p, npair * 4 - 1);
+    const int g = pc & 3, pr = pc >> 2, m = pr % M, b = b_begin + pr / M;
+    const h8 xv = *reinterpret_cast<const h8*>(X + ((size_t)(b * 4 + g) * 16 + m) * 8);
+    const float d = Xs[(size_t)b * mpad + m];
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int q[8], qsum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      q[e] = (int)__builtin_rintf((float)xv[e] * id);
+      qsum += q[e];
+    }
+    qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, true);  // quad xor 1
+    qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, true);  // quad xor 2
+    if (p < npair * 4) {
+      u32x2 wq;
+      if constexpr (BITS == 4) {
+        wq[0] = pack_i8x4(q[0], q[4], q[1], q[5]);
+        wq[1] = pack_i8x4(q[2], q[6], q[3], q[7]);
+      } else {
+        wq[0] = pack_i8x4(q[0], q[2], q[1], q[3]);
+        wq[1] = pack_i8x4(q[4], q[6], q[5], q[7]);
+      }
+      reinterpret_cast<u32x2*>(xq)[pr * 4 + g] = wq;
+      if (g == 0) {
+        xsum[pr] = qsum;
+        dsc[pr] = d;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. this wave's groups: block dots and scales into LDS
+  for (int base = bq_lo + wave; base <= bq_hi; base += 4 * GD) {
+#pragma unroll
+    for (int j = 0; j < GD; j++) {
+      const int bq = base + 4 * j;
+      const int b = bq * 4 + bb;
+      const bool in = b >= b_begin && b < b_end;  // false past bq_hi (clamped re-read)
+      const int bl = min(max(b - b_begin, 0), nblk - 1);
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        if constexpr (BITS == 4) {
+          lo[g] = wr[j][g] & 0x0F0F0F0Fu;
+          hi[g] = (wr[j][g] >> 4) & 0x0F0F0F0Fu;
+        } else {
+          lo[g] = wr[j][2 * g];
+          hi[g] = wr[j][2 * g + 1];
+        }
+      }
+      const float dw = (float)__builtin_bit_cast(_Float16, sr[j]);
+      if (base + 4 * GD <= bq_hi) load(j, bq + 4 * GD);
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const u32x4* xr = xq + (size_t)(bl * M + m) * 2;
+        const u32x4 x0 = xr[0], x1 = xr[1];
+        int raw = 0;
+        raw = __builtin_amdgcn_sdot4((int)lo[0], (int)x0[0], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)hi[0], (int)x0[1], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)lo[1], (int)x0[2], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)hi[1], (int)x0[3], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)lo[2], (int)x1[0], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)hi[2], (int)x1[1], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)lo[3], (int)x1[2], raw, false);
+        raw = __builtin_amdgcn_sdot4((int)hi[3], (int)x1[3], raw, false);
+        const int isum = BITS == 4 ? raw - 8 * xsum[bl * M + m] : raw;
+        if (in) tt[(bl * M + m) * 16 + nn] = (float)isum * dsc[bl * M + m];
+      }
+      if (in) dws[bl * 16 + nn] = dw;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // loads of waves without groups have returned
+  __syncthreads();
+
+  // 3. canonical chains: wave kq runs quarter kq, wave 0 adds the quarters
+  if (wave < NQ && lane < 16 * M) {
+    const int c = lane & 15, m = lane >> 4;
+    float acc = 0.0f;
+    const int e0 = wave * qs;
+#pragma unroll 4
+    for (int bl = e0; bl < e0 + qs; bl++) acc = __builtin_fmaf(tt[(bl * M + m) * 16 + c], dws[bl * 16 + c], acc);
+    pq[(wave * M + m) * 16 + c] = acc;
+  }
+  if constexpr (NQ > 1) __syncthreads();
+  if (wave == 0 && lane < 16 * M) {
+    const int c = lane & 15, m = lane >> 4;
+    float o;
+    if constexpr (NQ == 1) o = pq[m * 16 + c];
+    else if constexpr (NQ == 2) o = pq[m * 16 + c] + pq[(M + m) * 16 + c];
+    else o = (pq[m * 16 + c] + pq[(M + m) * 16 + c]) + (pq[(2 * M + m) * 16 + c] + pq[(3 * M + m) * 16 + c]);
+    if (m < m_rows) Y[(size_t)split * slice_stride + (size_t)m * ldy + (size_t)ct * 16 + c] = o;
+  }
+}
+
+hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                           int splits, size_t slice_stride) {
+  const int nb = w.k / 32;
+  if (m_rows < 1 || m_rows > 4 || w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4))
+    return hipErrorInvalidValue;
+  const int nq = 4 / splits, nblk = nq * (nb / 4);
+  const int M = m_rows <= 1 ? 1 : m_rows <= 2 ? 2 : 4;
+  const size_t lds = (size_t)nblk * M * 40 + (size_t)nblk * 64 * (M + 1) + (size_t)nq * M * 64;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  const int ngroups = nblk % 4 == 0 ? nblk / 4 : (nblk + 3) / 4 + 1;  // groups a split touches, at most
+  const dim3 grid(w.n / 16, splits);
+  const uint32_t* W = (const uint32_t*)w.w;
+#define RSTR_GV(M_, B_, Q_)                                                                                   \
+  do {                                                                                                        \
+    if (ngroups <= 8)                                                                                         \
+      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 2>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
+                         ldy, m_rows, slice_stride);                                                          \
+    else                                                                                                      \
+      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 8>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
+                         ldy, m_rows, slice_stride);                                                          \
+  } while (0)
+#define RSTR_GV_Q(M_, B_)                    \
+  do {                                       \
+    if (nq == 4) RSTR_GV(M_, B_, 4);         \
+    else if (nq == 2) RSTR_GV(M_, B_, 2);    \
+    else RSTR_GV(M_, B_, 1);                 \
+  } while (0)
+#define RSTR_GV_M(B_)                        \
+  do {                                       \
+    if (M == 1) RSTR_GV_Q(1, B_);            \
+    else if (M == 2) RSTR_GV_Q(2, B_);       \
+    else RSTR_GV_Q(4, B_);                   \
+  } while (0)
+  if (w.bits == 4) RSTR_GV_M(4);
+  else if (w.bits == 8) RSTR_GV_M(8);
+  else return hipErrorInvalidValue;
+#undef RSTR_GV_M
+#undef RSTR_GV_Q
+#undef RSTR_GV
+  return hipGetLastError();
+}
+
 namespace {
 struct QgPlan {
   int rt, ct, nq;
@@ -834,13 +1021,26 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   const int nb = w.k / 32;
   if (w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4)) return hipErrorInvalidValue;
   if (w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
-  // One row against a long K (the MLP down projection): the weight-streaming
-  // GEMV.  Measured on MI355X at one row (Llama-3-8B shapes, weights streamed
-  // from HBM): down 4096 x 14336 13.8 us against 19.0 us for the 16-row MFMA
-  // tile; at K = 4096 the MFMA tile is as fast or faster (qkv 7.1 vs 7.6 us,
-  // gate/up 16.0 vs 17.6 us), and at two or more rows it wins everywhere.
-  if (x.mpad == 16 && m_rows == 1 && w.k >= 8192 && launch_qgemv(st, w, x, m_rows, y, ldy, splits, slice_stride) == hipSuccess)
-    return hipSuccess;
+  // Few rows: the weight-streaming GEMVs.  Measured on MI355X (weights streamed
+  // from HBM, four K slices; us for the GEMV forms against the 16-row MFMA
+  // tile): one row against a long K (the MLP down projection, 4096 x 14336)
+  // takes k_qgemv, 12.8 us (13.6 for the workgroup form, 19.0 for the tile);
+  // other shapes at one or two rows take the workgroup form k_qgemv_wg --
+  // Llama-3-8B qkv 6.4 vs 7.1, o 5.5 vs 5.8, gate/up 15.6 vs 16.0 (Q8: 7.9 vs
+  // 9.1, 6.5 vs 8.2, 23.7 vs 26.7), down at two rows 14.9 vs 19.8, Qwen3-0.6B
+  // down 3.7 vs 4.7, Gemma-3-270M down 3.3 vs 4.0; at three and four rows the
+  // tile wins on the 4096-wide shapes (o 6.7 vs 5.8) and the workgroup form
+  // only on matrices up to 4M weights (Qwen3-0.6B down 4.3 vs 4.8).  Quarters
+  // that are not whole 4-block groups (K = 640: Gemma-3-270M) stay on the tile,
+  // whose preloaded chains were faster there (config1 0.750 vs 0.760 ms/step).
+  if (x.mpad == 16 && m_rows <= 4) {
+    if (m_rows == 1 && w.k >= 8192) {
+      if (launch_qgemv(st, w, x, m_rows, y, ldy, splits, slice_stride) == hipSuccess) return hipSuccess;
+    } else if (splits == 4 && (nb / 4) % 4 == 0 &&
+               (m_rows <= 2 || (size_t)w.n * (size_t)w.k <= ((size_t)4 << 20))) {
+      if (launch_qgemv_wg(st, w, x, m_rows, y, ldy, splits, slice_stride) == hipSuccess) return hipSuccess;
+    }
+  }
   const QgPlan p = qg_plan(x.mpad, splits, w.bits, nb);
   const int nct = w.n / 16;
   const int mt_all = x.mpad / 16;

@@ -596,6 +596,23 @@ def test_one_lane_long_k_weight_streaming(sess, bits):
     _close(r)
 
 
+@pytest.mark.parametrize("name,B,bits", [("llama3_8b", 2, 4), ("llama3_8b", 2, 8), ("llama3_8b", 4, 4),
+                                         ("qwen3_06b", 4, 8), ("gemma3_270m", 3, 8)])
+def test_few_lane_weight_streaming(sess, name, B, bits):
+    """Two to four lanes at full config width (first layer, full vocabulary):
+    projections with four K slices run on the workgroup GEMV at two rows, and at
+    three or four rows for matrices up to 4M weights (the rest on the MFMA
+    tile); tokens and logits equal the oracle's on every step."""
+    print(f"case few lanes {name} B={B} q{bits}", flush=True)
+    cfg = configs.with_bits(_cfg(name, n_layers=1), bits)
+    prefix = [300, 0, 17, 120][:B]
+    r = _run_lanes(sess, cfg, B, prefix, [list(range(B))] * 3, split=256, ps=16, pages=80, pps=30, maxpos=400)
+    try:
+        assert np.array_equal(r["d"].rows(), r["od"].r0())
+    finally:
+        _close(r)
+
+
 @pytest.mark.parametrize("name,layers", [("llama3_8b", 1), ("gemma3_270m", 6), ("qwen3_06b", 1)])
 def test_config_shapes_first_layers(sess, name, layers):
     """Full-width config shapes (vocabulary included) with the first layers only:
