@@ -668,7 +668,9 @@ __global__ __launch_bounds__(64 * WV) void k_qgemv(const uint32_t* __restrict__ 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // the clamped re-reads past the end have returned
   __syncthreads();
 
-  // 3. canonical chain, one lane per (column, row)
+  // 3. canonical chain, one lane per (column, row); unrolled 16 deep so that
+  // many of the chain's LDS reads are in flight at once (one-row down
+  // 4096 x 14336: 12.8 -> 12.2 us)
   if (lane < 16 * M) {
     const int c = lane & 15, m = lane >> 4;
     float part[NQ];
@@ -676,7 +678,7 @@ __global__ __launch_bounds__(64 * WV) void k_qgemv(const uint32_t* __restrict__ 
     for (int kq = 0; kq < NQ; kq++) {
       float acc = 0.0f;
       const int e0 = kq * qs;
-#pragma unroll 4
+#pragma unroll 16
       for (int bl = e0; bl < e0 + qs; bl++) acc = __builtin_fmaf(tt[(bl * M + m) * 16 + c], dws[bl * 16 + c], acc);
       part[kq] = acc;
     }
@@ -863,7 +865,7 @@ __global__ __launch_bounds__(256) void k_qgemv_wg(const uint32_t* __restrict__ W
     const int c = lane & 15, m = lane >> 4;
     float acc = 0.0f;
     const int e0 = wave * qs;
-#pragma unroll 4
+#pragma unroll 16
     for (int bl = e0; bl < e0 + qs; bl++) acc = __builtin_fmaf(tt[(bl * M + m) * 16 + c], dws[bl * 16 + c], acc);
     pq[(wave * M + m) * 16 + c] = acc;
   }
