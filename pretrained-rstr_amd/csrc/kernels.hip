@@ -2842,7 +2842,24 @@ __global__ __launch_bounds__(64) void k_argmax_final(const int32_t* __restrict__
   if (lane == 0) tok[row] = t;
   const float* er = emb + (size_t)t * d;
   float* rr = r0 + (size_t)row * d;
-  for (int i = lane; i < d; i += 64) rr[i] = er[i];
+  if ((d & 3) == 0) {
+    // 16-byte pieces, eight loads in flight per lane before their stores (a
+    // load-then-store loop waits one memory round trip per 256 bytes of row:
+    // 26 us for a 4096-wide row)
+    const f4* e4 = reinterpret_cast<const f4*>(er);
+    f4* r4 = reinterpret_cast<f4*>(rr);
+    const int n4 = d >> 2;
+    for (int i0 = lane; i0 < n4; i0 += 8 * 64) {
+      f4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = e4[min(i0 + 64 * j, n4 - 1)];
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        if (i0 + 64 * j < n4) r4[i0 + 64 * j] = v[j];
+    }
+  } else {
+    for (int i = lane; i < d; i += 64) rr[i] = er[i];
+  }
 }
 
 hipError_t launch_argmax_gather(hipStream_t st, const float* logits, int rows, int vocab,
@@ -2859,7 +2876,22 @@ __global__ void k_gather_rows(const float* __restrict__ emb, int d, const int32_
   const int i = blockIdx.x;
   const float* er = emb + (size_t)tokens[i] * d;
   float* rr = r0 + (size_t)lanes[i] * d;
-  for (int k = threadIdx.x; k < d; k += blockDim.x) rr[k] = er[k];
+  if ((d & 3) == 0) {
+    // 16-byte pieces, four loads in flight per thread before their stores
+    const f4* e4 = reinterpret_cast<const f4*>(er);
+    f4* r4 = reinterpret_cast<f4*>(rr);
+    const int n4 = d >> 2, nt = blockDim.x;
+    for (int k0 = threadIdx.x; k0 < n4; k0 += 4 * nt) {
+      f4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = e4[min(k0 + nt * j, n4 - 1)];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (k0 + nt * j < n4) r4[k0 + nt * j] = v[j];
+    }
+  } else {
+    for (int k = threadIdx.x; k < d; k += blockDim.x) rr[k] = er[k];
+  }
 }
 
 hipError_t launch_gather_rows(hipStream_t st, const float* emb, int d, const int32_t* lanes,
