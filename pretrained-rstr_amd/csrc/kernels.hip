@@ -1552,6 +1552,24 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     for (int i = tid; i < RSTR_NCH; i += 1024) s_h[i] = 0;
     __syncthreads();
   }
+  // list offsets of the partial items by decreasing chunk count: boff[c] =
+  // the partial items of all counts above c, an exclusive suffix sum over s_h
+  // (inclusive scan over the reversed counts; thread r holds count NCH-1-r)
+  static_assert(RSTR_NCH <= 1024, "one count per thread");
+  const int32_t hv = tid < RSTR_NCH ? s_h[RSTR_NCH - 1 - tid] : 0;
+  s_a[tid] = hv;
+  __syncthreads();
+  for (int off = 1; off < RSTR_NCH; off <<= 1) {
+    const int32_t t = tid >= off ? s_a[tid - off] : 0;
+    __syncthreads();
+    s_a[tid] += t;
+    __syncthreads();
+  }
+  if (tid < RSTR_NCH) {
+    int32_t* boff = tab + attn_bucket_offset(batch);
+    boff[RSTR_NCH - 1 - tid] = s_a[tid] - hv;
+    boff[RSTR_NCH + (RSTR_NCH - 1 - tid)] = 0;  // fill cursor
+  }
   if (tid == 0) {
     base[batch] = carry_a;
     fbase[batch] = carry_f;
@@ -1561,14 +1579,6 @@ __global__ __launch_bounds__(1024) void k_attn_prep(int batch, int split, int wi
     const int arm = attn_static_rounds(carry_a, R) * R;
     tab[attn_ctl_offset(batch)] = arm;
     tab[attn_ctl_offset(batch) + 1] = arm;
-    // list offsets of the partial items by decreasing chunk count
-    int32_t acc = 0;
-    int32_t* boff = tab + attn_bucket_offset(batch);
-    for (int c = RSTR_NCH - 1; c >= 0; c--) {
-      boff[c] = acc;
-      boff[RSTR_NCH + c] = 0;  // fill cursor
-      acc += s_h[c];
-    }
   }
 }
 
@@ -1588,17 +1598,26 @@ __global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int spl
   const int32_t* base = tab + 3 * batch;
   const int32_t* fbase = tab + 4 * batch + 1;
   const int32_t* pbase = tab + 5 * batch + 2;
+  // the lane prefix in LDS for the search below (a search through global
+  // memory is a chain of dependent round trips)
+  constexpr int SB = 2048;
+  __shared__ int32_t s_base[SB];
+  const bool lds = batch < SB;
+  if (lds)
+    for (int k = threadIdx.x; k <= batch; k += 256) s_base[k] = base[k];
+  __syncthreads();
+  const int32_t* sb = lds ? s_base : base;
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= base[batch]) return;
+  if (i >= sb[batch]) return;
   // the last lane whose first item is <= i (lanes without items have
   // base[b] == base[b+1], so the search lands on the lane that holds i)
   int b = 0, hi = batch;
   while (hi - b > 1) {
     const int mid = (b + hi) >> 1;
-    if (base[mid] <= i) b = mid; else hi = mid;
+    if (sb[mid] <= i) b = mid; else hi = mid;
   }
   const int ns = ns_t[b];
-  const int rel = i - base[b];
+  const int rel = i - sb[b];
   const int kvh = rel / ns;
   const int s = rel % ns;
   const int len = lengths[b];
