@@ -597,12 +597,13 @@ def test_one_lane_long_k_weight_streaming(sess, bits):
 
 
 @pytest.mark.parametrize("name,B,bits", [("llama3_8b", 2, 4), ("llama3_8b", 2, 8), ("llama3_8b", 4, 4),
-                                         ("qwen3_06b", 4, 8), ("gemma3_270m", 3, 8)])
+                                         ("qwen3_06b", 4, 8), ("qwen3_06b", 2, 4), ("gemma3_270m", 3, 8)])
 def test_few_lane_weight_streaming(sess, name, B, bits):
     """Two to four lanes at full config width (first layer, full vocabulary):
     projections with four K slices run on the workgroup GEMV at two rows, and at
-    three or four rows for matrices up to 4M weights (the rest on the MFMA
-    tile); tokens and logits equal the oracle's on every step."""
+    three or four rows for matrices up to 4M weights, and the Qwen3 head (one
+    slice, K = 1024) at two rows (the rest on the MFMA tile); tokens and logits
+    equal the oracle's on every step."""
     print(f"case few lanes {name} B={B} q{bits}", flush=True)
     cfg = configs.with_bits(_cfg(name, n_layers=1), bits)
     prefix = [300, 0, 17, 120][:B]
