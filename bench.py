@@ -47,6 +47,11 @@ WORKLOADS = {
 }
 
 
+# workloads whose route pages are a seeded random permutation of the physical pool
+# ("Page tables are a random permutation of the physical page
+# pool"; SURVEY seed 1): the pool's own ids map through workload.PermutedPages
+PAGE_PERM_SEEDS = {"config2": 1}
+
 # isolated attention workloads: (model shape, lanes, seed)
 ATTN_WORKLOADS = {"config4": ("llama3_8b", 128, 4)}
 
@@ -521,7 +526,8 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
     host bookkeeping and the boundary call separated."""
     dev = workload.LiveDevice(dec, pool)
     planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed + 1000, arrival_mean=arrivals,
-                                    prompt=prompt, output=output, device=dev)
+                                    prompt=prompt, output=output, device=dev,
+                                    page_perm_seed=PAGE_PERM_SEEDS.get(args.workload))
     for _ in range(2):  # admissions of the steady-state start, first graph replays
         planner.plan_step()
     dev.step_seconds = dev.other_seconds = 0.0
@@ -655,7 +661,8 @@ def _decode_workload(args, sess) -> dict:
         planner = workload.SharedPrefixPlanner(cfg, lanes, ps, physical, maxpos, seed=seed)
     else:
         planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed, arrival_mean=arrivals,
-                                        prompt=prompt, output=output)
+                                        prompt=prompt, output=output,
+                                        page_perm_seed=PAGE_PERM_SEEDS.get(args.workload))
     t0 = time.perf_counter()
     plan = [planner.plan_step() for _ in range(n_total)]
     plan_s = time.perf_counter() - t0
@@ -735,7 +742,10 @@ def _decode_workload(args, sess) -> dict:
                 + ("Poisson churn)" if prompt is not None else "shared-prefix forks)"),
         "config": {"workload": (f"{args.workload}: {name}-shaped Q4 decoder, {lanes} continuous lanes, "
                                 f"prompts U{list(prompt)}, outputs U{list(output)}, "
-                                f"Poisson({arrivals}) arrivals/step") if prompt is not None else
+                                f"Poisson({arrivals}) arrivals/step"
+                                + (f", route pages a seeded permutation of the physical pool (seed "
+                                   f"{PAGE_PERM_SEEDS[args.workload]})" if args.workload in PAGE_PERM_SEEDS else
+                                   ", pages lowest-free-first")) if prompt is not None else
                                (f"{args.workload}: {name}-shaped Q4 decoder, {lanes} decode lanes, contexts "
                                 f"log-uniform[256, 8192], lanes 0-31 fork one 1024-token prefix "
                                 f"(copy-on-write on the first divergent append); {planner.cow_pages} pages copied"),

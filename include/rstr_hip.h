@@ -261,8 +261,12 @@ int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, int32_t n_q, 
                        const int32_t* positions, const int32_t* page_table, int32_t pages_per_seq,
                        const int32_t* lengths, const int32_t* start_positions, float* out);
 /* No counterpart in the reference.  For callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc): rstr_attention_run's arguments, validation, kernels and
+ * memory (tight serving loops, harnesses that forbid hipMalloc, code that
+ * must not allocate while a graph elsewhere is being captured): it is
+ * allocation-free, not capturable -- it copies the host arrays in and the
+ * output back with blocking copies and synchronises the session stream, so it
+ * must be called outside any active stream capture.  rstr_attention_run's
+ * arguments, validation, kernels and
  * results, with no hipMalloc/hipFree -- the query, descriptors, work tables,
  * split partials and output are staged in one library-owned device array of
  * RSTR_ATTN_STATIC_BYTES on each GPU (held until the process ends; its address

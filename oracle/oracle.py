@@ -65,6 +65,7 @@ def lib():
             "orc_quant_q4": (None, [P, i64, i64, P, P]),
             "orc_quant_q8": (None, [P, i64, i64, P, P]),
             "orc_act_scale": (f32, [f32]),
+            "orc_set_act_scale_plain": (None, [i32]),
             "orc_quant_act": (None, [P, i32, i32, P, P]),
             "orc_qlinear": (None, [i32, P, P, i32, i32, P, P, i32, P]),
             "orc_sumsq": (f32, [P, i32]),
@@ -83,6 +84,7 @@ def lib():
             "orc_decoder_open": (P, [P, i32, i32, i32, i32, i32, i32, i32]),
             "orc_decoder_free": (None, [P]),
             "orc_prime_lanes": (None, [P, i32, P, P]),
+            "orc_prime_rows": (None, [P, i32, P, P]),
             "orc_step_lanes": (i32, [P, P, P, P, P, P, P, P]),
             "orc_logits": (P, [P]),
             "orc_r0": (P, [P]),
@@ -301,6 +303,10 @@ class Decoder:
     def prime_lanes(self, lanes, tokens):
         lanes, tokens = i32(lanes), i32(tokens)
         lib().orc_prime_lanes(self.h, len(lanes), ptr(lanes), ptr(tokens))
+
+    def prime_rows(self, lanes, rows):
+        lanes, rows = i32(lanes), f32(rows)
+        lib().orc_prime_rows(self.h, lanes.size, ptr(lanes), ptr(rows))
 
     def step_lanes(self, slots, row_offsets, positions, page_table, lengths, start_positions):
         out = np.empty(self.batch, np.int32)

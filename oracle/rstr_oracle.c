@@ -249,9 +249,17 @@ void orc_quant_q8(const float* w, int64_t rows, int64_t cols, int8_t* q, uint16_
 /* then q*d is an exact fp16 value for every |q| <= 127 (7 + 4 significant   */
 /* bits, at least 2^-24, at most 60960), which lets the linear fold d into    */
 /* its integer block dot exactly.  An all-zero block has d = 0.               */
+/* Measurement hook (tests only): 1 selects the plain scale RN(amax/127), with */
+/* no significand rounding and no clamps, the most direct reading of          */
+/* qlinear-i8's d = amax/127; 0 (the default) selects the scale above.  With  */
+/* the plain scale isum*dx rounds to fp32 in the linear.                      */
+static int g_act_scale_plain = 0;
+void orc_set_act_scale_plain(int32_t on) { g_act_scale_plain = on != 0; }
+
 float orc_act_scale(float amax) {
   if (!(amax > 0.0f)) return 0.0f;
   float d = amax / 127.0f;
+  if (g_act_scale_plain) return d;
   uint32_t b;
   memcpy(&b, &d, 4);
   if (b & 0xFFFFFu) b = (b & ~0xFFFFFu) + 0x100000u;   /* round up to 4 significant bits */
@@ -332,7 +340,7 @@ void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out
           int32_t isum = (bits == 4)
                              ? dot_q4((const uint8_t*)wq + ((int64_t)n * nb + b) * 16, xr + 32 * b)
                              : dot_q8((const int8_t*)wq + ((int64_t)n * nb + b) * 32, xr + 32 * b);
-          float t = (float)isum * sr[b];   /* exact */
+          float t = (float)isum * sr[b];   /* exact (RN with the plain-scale hook) */
           acc = fmaf(t, dw[b], acc);
         }
         quarter[q] = acc;
@@ -788,6 +796,13 @@ void orc_decoder_free(orc_decoder* d) {
 void orc_prime_lanes(orc_decoder* d, int32_t n, const int32_t* lanes, const int32_t* tokens) {
   for (int32_t i = 0; i < n; i++)
     orc_embed_row(d->m, tokens[i], d->r0 + (int64_t)lanes[i] * d->m->d.d_model);
+}
+
+/* Arbitrary f32 input rows for the given lanes (rstr_prime_rows' semantics). */
+void orc_prime_rows(orc_decoder* d, int32_t n, const int32_t* lanes, const float* rows) {
+  const int32_t dm = d->m->d.d_model;
+  for (int32_t i = 0; i < n; i++)
+    memcpy(d->r0 + (int64_t)lanes[i] * dm, rows + (int64_t)i * dm, sizeof(float) * (size_t)dm);
 }
 
 const float* orc_logits(const orc_decoder* d) { return d->logits; }

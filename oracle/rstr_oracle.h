@@ -71,6 +71,7 @@ void orc_normal_fill(uint64_t key, uint64_t start, int64_t n, double mean, doubl
 void orc_quant_q4(const float* w, int64_t rows, int64_t cols, uint8_t* nib, uint16_t* scales);
 void orc_quant_q8(const float* w, int64_t rows, int64_t cols, int8_t* q, uint16_t* scales);
 float orc_act_scale(float amax);
+void orc_set_act_scale_plain(int32_t on);   /* measurement hook: plain RN(amax/127) */
 void orc_quant_act(const float* x, int32_t rows, int32_t cols, int8_t* q, float* scales);
 void orc_qlinear(int32_t bits, const void* wq, const uint16_t* ws, int32_t n_out, int32_t k_in,
                  const int8_t* xq, const float* xs, int32_t rows, float* y);
@@ -106,6 +107,7 @@ orc_decoder* orc_decoder_open(const orc_model* m, int32_t batch, int32_t page_si
                               int32_t kv_f16, int32_t split);
 void orc_decoder_free(orc_decoder* d);
 void orc_prime_lanes(orc_decoder* d, int32_t n, const int32_t* lanes, const int32_t* tokens);
+void orc_prime_rows(orc_decoder* d, int32_t n, const int32_t* lanes, const float* rows);
 int32_t orc_step_lanes(orc_decoder* d, const int32_t* slots, const int32_t* row_offsets,
                        const int32_t* positions, const int32_t* page_table,
                        const int32_t* lengths, const int32_t* start_positions,

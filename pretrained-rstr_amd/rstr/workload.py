@@ -107,19 +107,69 @@ class LiveDevice:
         return self._tokens
 
 
+class PermutedPages:
+    """Device protocol wrapper that places the pool's pages at a fixed permutation
+    of the physical page pool: page p of the control plane is physical page
+    ``perm[p]`` in every fill, copy-on-write copy, slot and page-table entry the
+    wrapped device sees.  The pool keeps its lowest-free-first order
+    (page_pool.clj:513-524) over its own ids, so route tables land on scattered
+    physical pages, as a long-running pool's free list leaves them (BASELINE.json
+    page tables are a random permutation of the physical pool)."""
+
+    def __init__(self, inner, physical_pages: int, page_size: int, seed: int):
+        self.inner, self.page_size = inner, int(page_size)
+        self.perm = np.random.default_rng(seed).permutation(int(physical_pages)).astype(np.int32)
+
+    def begin(self):
+        self.inner.begin()
+
+    def end(self):
+        return self.inner.end()
+
+    def copy_page(self, src, dst):
+        self.inner.copy_page(int(self.perm[src]), int(self.perm[dst]))
+
+    def fill(self, pages):
+        self.inner.fill([int(self.perm[p]) for p in pages])
+
+    def prime_rows(self, lane_tokens):
+        self.inner.prime_rows(lane_tokens)
+
+    def upload(self, desc):
+        d = dict(desc)
+        ps = self.page_size
+        slots = np.asarray(desc["slots"], np.int64)
+        d["slots"] = np.where(slots >= 0, self.perm[np.maximum(slots, 0) // ps].astype(np.int64) * ps + slots % ps,
+                              slots).astype(np.int32)
+        pt = np.asarray(desc["page_table"], np.int64)
+        d["page_table"] = np.where(pt >= 0, self.perm[np.maximum(pt, 0)], pt).astype(np.int32)
+        self.inner.upload(d)
+
+    def run(self):
+        self.inner.run()
+
+    def download_tokens(self):
+        return self.inner.download_tokens()
+
+
 class ChurnPlanner:
     """Poisson arrivals, uniform prompt/output lengths, fixed lanes, fixed page pool.
     ``device`` executes the plan as it is made (``LiveDevice``); by default the
-    steps are recorded for a device-resident schedule."""
+    steps are recorded for a device-resident schedule.  ``page_perm_seed`` places
+    the pool's pages at a seeded permutation of the physical pool
+    (``PermutedPages``)."""
 
     def __init__(self, cfg: dict, batch: int, page_size: int, physical_pages: int, maxpos: int,
                  seed: int, arrival_mean: float = 4.0, prompt=(128, 4096), output=(32, 512),
-                 fill_seed: int = 7, warm_start: bool = True, retain_finished: bool = False, device=None):
+                 fill_seed: int = 7, warm_start: bool = True, retain_finished: bool = False, device=None,
+                 page_perm_seed: int | None = None):
         self.cfg, self.batch, self.maxpos = cfg, batch, maxpos
         self.rng = np.random.default_rng(seed)
         self.arrival_mean, self.prompt, self.output = arrival_mean, prompt, output
         self.fill_seed = fill_seed
         self.rec = device if device is not None else RecordingDevice()
+        if page_perm_seed is not None:
+            self.rec = PermutedPages(self.rec, physical_pages, page_size, page_perm_seed)
         self.pool = PagePool(page_size, physical_pages, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"],
                              device=self.rec)
         self.dec = PagedDecoder(self.pool, self.rec, batch_size=batch, maxpos=maxpos)

@@ -3,12 +3,14 @@ bench's host-planned schedules replayed on the HIP decoder (fills, copy-on-write
 copies, primes, one step graph per step) and on the oracle, token for token.
 
 - config2: Gemma-3-270M-shaped Q4 (18 layers, sliding window 512), 16 lanes,
-  contexts U[64, 2048] admitted onto a permuted page pool (attention split 64).
+  contexts U[64, 2048], route pages at a seeded permutation of the physical pool
+  (seed 1, as the bench runs it), attention split 32 (the bench's split).
 - config3: Qwen3-0.6B-shaped Q4 (28 layers, qk-norm), 64 lanes, contexts
   log-uniform [256, 8192], lanes 0-31 forking one 1024-token prefix with
   copy-on-write on their first divergent append (attention split 128).
 - config5: Llama-3-8B-shaped Q4 (32 layers), 128 lanes with churn (prompts capped
-  at 1024 tokens to bound the oracle's host KV memory)."""
+  at 1024 tokens to bound the oracle's host KV memory), and a few lanes at the
+  bench's full prompt range (contexts of 3500-4096 tokens through all 32 layers)."""
 import numpy as np
 import pytest
 
@@ -48,9 +50,13 @@ def test_config2_shape_schedule_matches_oracle():
     batch, maxpos = 16, 2048 + 64
     pages = 16 * (maxpos // 16 + 1) + 64
     pl = workload.ChurnPlanner(cfg, batch, 16, pages, maxpos, seed=1, arrival_mean=0.0,
-                               prompt=(64, 2048), output=(256, 256))
-    steps = _replay(cfg, pl, batch, pages, maxpos, 64, 3)
+                               prompt=(64, 2048), output=(256, 256), page_perm_seed=1)
+    steps = _replay(cfg, pl, batch, pages, maxpos, 32, 3)
     assert max(max(st["lengths"]) for st in steps) > 512  # windowed layers see a partial window
+    # route pages are scattered over the physical pool, not lowest-first runs
+    pt = np.asarray(steps[-1]["page_table"])
+    first = pt[:, 0][pt[:, 0] >= 0]
+    assert len(set(first.tolist())) == len(first) and first.max() > pages // 2
 
 
 def test_config3_shape_schedule_matches_oracle():
@@ -77,3 +83,20 @@ def test_config5_shape_one_step_matches_oracle():
                                prompt=(128, 1024), output=(32, 64))
     steps = _replay(cfg, pl, batch, pages, maxpos, 256, 2)
     assert all(st["active"] == batch for st in steps)
+
+
+def test_config5_shape_full_context_lanes_match_oracle():
+    """The north-star model with lanes at the bench's full prompt range: 8 lanes
+    whose prompts are drawn from U[3500, 4096] (restored prefixes of 3499-4095
+    rows), all 32 layers and the head, two planned steps, every lane's tokens
+    equal to the oracle's.  Attention runs the many-item split kernel (17 splits of
+    256 tokens per lane and kv head)."""
+    print("case config5 full context", flush=True)
+    cfg = configs.LLAMA3_8B
+    batch, maxpos = 8, 4096 + 64
+    pages = batch * (maxpos // 16 + 1)
+    pl = workload.ChurnPlanner(cfg, batch, 16, pages, maxpos, seed=5, arrival_mean=0.0,
+                               prompt=(3500, 4096), output=(32, 64))
+    steps = _replay(cfg, pl, batch, pages, maxpos, 256, 2)
+    assert all(st["active"] == batch for st in steps)
+    assert min(min(st["lengths"]) for st in steps) >= 3500

@@ -720,3 +720,91 @@ def test_decode_matches_golden_fixture(sess, case):
         d.close()
         p.close()
         m.close()
+
+
+# ---------------------------------------------------------------------------
+# activation blocks outside the scale's [2^-21, 480] range
+# ---------------------------------------------------------------------------
+def _clamp_case(sess, v_big, plain=False, hip_side=True):
+    """Two lanes of tiny_llama.  Lane 0 attends over 60 restored rows whose V
+    holds v_big in dims 0..31 of kv head 0 (every layer), so its attention
+    output there -- the O projection's input -- lies above 127*480 = 60960.  Lane
+    1's input row has a block of 1e-9 (dims 32..63) and one of 1e-6 (64..95), so
+    its first normed row carries blocks below 2^-22 and near 2^-20."""
+    cfg = configs.TINY_LLAMA
+    B, ps, pages, pps, maxpos, split = 2, 16, 8, 4, 64, 16
+    pt = np.array([[0, 1, 2, 3], [4, 5, -1, -1]], np.int32)
+    lengths = np.array([61, 21], np.int32)
+    pos = lengths - 1
+    slots = np.array([pt[b, pos[b] // ps] * ps + pos[b] % ps for b in range(B)], np.int32)
+    rows = np.arange(B + 1, dtype=np.int32)
+    row1 = np.random.default_rng(3).standard_normal(cfg["d_model"]).astype(np.float32)
+    row1[32:64] = np.linspace(-1e-9, 1e-9, 32, dtype=np.float32)
+    row1[64:96] = np.linspace(-1e-6, 1e-6, 32, dtype=np.float32)
+    big = np.zeros((4, ps, cfg["head_dim"]), np.float16)
+
+    def setup(fill, vset, prime_tok, prime_row):
+        for pg in range(pages):
+            fill(pg)
+        for layer in range(cfg["n_layers"]):
+            vset(layer)
+        prime_tok()
+        prime_row()
+
+    out = {}
+    om = O.Model(cfg, seed=2)
+    od = O.Decoder(om, B, ps, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        if plain:
+            O.lib().orc_set_act_scale_plain(1)
+
+        def o_vset(layer):
+            v = od.slab(1, layer)
+            v[0:4, :, 0, 0:32] = np.float16(v_big)
+
+        setup(lambda pg: od.fill_synthetic(pg, 5), o_vset, lambda: od.prime_lanes([0], [7]),
+              lambda: od.prime_rows([1], row1[None]))
+        out["oracle"] = (od.step_lanes(slots, rows, pos, pt, lengths, np.zeros(B, np.int32)), od.logits(),
+                         od.r0())
+    finally:
+        O.lib().orc_set_act_scale_plain(0)
+        od.close()
+    if hip_side:
+        m = hip.Model(sess, cfg, seed=2)
+        p = hip.Pool(m, ps, pages)
+        d = hip.Decoder(m, p, B, pps, maxpos, split)
+        try:
+            def h_vset(layer):
+                v = p.pages(1, layer).copy()
+                v[0:4, :, 0, 0:32] = np.float16(v_big)
+                p.upload(1, layer, 0, v[0:4])
+
+            setup(lambda pg: p.fill_synthetic([pg], 5), h_vset, lambda: d.prime_lanes([0], [7]),
+                  lambda: d.prime_rows([1], row1[None]))
+            out["hip"] = (d.step_lanes(slots, rows, pos, pt, lengths, np.zeros(B, np.int32)), d.logits(), d.rows())
+        finally:
+            d.close(); p.close(); m.close()
+    # the first normed row of lane 1 (the layer-0 qkv input) has the intended blocks
+    g = om.norm(0, "attn_norm")
+    h = O.rmsnorm(row1[None], g, float(cfg["gain_offset"]), float(cfg["eps"]))[0]
+    om.close()
+    assert np.abs(h[32:64]).max() < 2.0 ** -22 and 2.0 ** -22 < np.abs(h[64:96]).max() < 2.0 ** -19
+    return out
+
+
+def test_activation_scale_clamp_regimes_match_the_oracle(sess):
+    """Activation blocks above 60960 saturate (q = +-127 at d = 480) and blocks
+    below 2^-22 quantise to zero, on the GPU exactly as in the oracle: tokens,
+    logits and next input rows bit for bit.  Saturation is shown end to end: V
+    rows of 65504 and of 64512 give the same step (every value of the block
+    clamps), while the plain amax/127 scale tells them apart."""
+    print("case activation scale clamps", flush=True)
+    a = _clamp_case(sess, 65504.0)
+    b = _clamp_case(sess, 64512.0)
+    for r in (a, b):
+        for got, want in zip(r["hip"], r["oracle"]):
+            assert np.array_equal(np.asarray(got).view(np.uint32), np.asarray(want).view(np.uint32))
+    assert np.array_equal(a["hip"][1].view(np.uint32), b["hip"][1].view(np.uint32))
+    pa = _clamp_case(sess, 65504.0, plain=True, hip_side=False)
+    pb = _clamp_case(sess, 64512.0, plain=True, hip_side=False)
+    assert not np.array_equal(pa["oracle"][1][0], pb["oracle"][1][0])

@@ -48,3 +48,36 @@ def test_planner_keeps_the_pool_consistent(retain):
     else:
         assert pl.evicted == 0
         assert set(pl.pool.routes) == active
+
+
+def test_permuted_pages_map_every_page_reference_consistently():
+    """``page_perm_seed`` places the pool's pages at a seeded permutation of the
+    physical pool: fills, copy-on-write pairs, slots and page-table entries all go
+    through the same bijection, so a lane's slot lies in its own mapped page
+    table and the recorded steps equal the unpermuted plan mapped page by page."""
+    import numpy as np
+
+    kw = dict(batch=6, page_size=16, physical_pages=160, maxpos=200, seed=11, arrival_mean=1.5,
+              prompt=(8, 60), output=(2, 12))
+    plain = ChurnPlanner(CFG, **kw)
+    perm_pl = ChurnPlanner(CFG, **kw, page_perm_seed=1)
+    perm = np.random.default_rng(1).permutation(160)
+    assert sorted(perm.tolist()) == list(range(160)) and (perm != np.arange(160)).any()
+    moved = 0
+    for _ in range(40):
+        a, b = plain.plan_step(), perm_pl.plan_step()
+        assert b["fill_pages"] == [int(perm[p]) for p in a["fill_pages"]]
+        assert [tuple(x) for x in b["cow_pairs"]] == [(int(perm[s]), int(perm[d])) for s, d in a["cow_pairs"]]
+        pt_a, pt_b = np.asarray(a["page_table"]), np.asarray(b["page_table"])
+        assert np.array_equal(pt_b, np.where(pt_a >= 0, perm[np.maximum(pt_a, 0)], -1))
+        sa, sb = np.asarray(a["slots"]), np.asarray(b["slots"])
+        assert np.array_equal(sb < 0, sa < 0) and np.array_equal(sb % 16, sa % 16)
+        assert np.array_equal(sb[sa >= 0] // 16, perm[sa[sa >= 0] // 16])
+        for k in ("lengths", "start_positions", "positions", "row_offsets"):
+            assert np.array_equal(np.asarray(a[k]), np.asarray(b[k])), k
+        for lane in np.nonzero(np.asarray(b["lengths"]) > 0)[0]:
+            # the appended row's page is one of the lane's own visible pages
+            n = int(b["lengths"][lane])
+            assert sb[lane] // 16 == pt_b.reshape(6, -1)[lane, (n - 1) // 16]
+        moved += int((pt_b[pt_b >= 0] != pt_a[pt_a >= 0]).sum())
+    assert moved > 0
