@@ -78,6 +78,7 @@ def lib():
             "orc_argmax_rows": (None, [P, i32, i32, P]),
             "orc_model_synthetic": (P, [P, u64]),
             "orc_model_free": (None, [P]),
+            "orc_model_set_tensor": (i32, [P, i32, i32, P, i64]),
             "orc_model_tensor": (i64, [P, i32, i32, P, P]),
             "orc_model_norm": (i64, [P, i32, i32, P]),
             "orc_embed_row": (None, [P, i32, P]),
@@ -255,6 +256,12 @@ class Model:
         ws = np.empty((n, k // 32), np.uint16)
         lib().orc_model_tensor(self.h, layer, ROLE[role], ptr(wq), ptr(ws))
         return wq, ws
+
+    def set_tensor(self, layer: int, role: str, values) -> None:
+        """Replace one tensor by host values (e.g. a checkpoint's, widened to f32)."""
+        v = f32(values).ravel()
+        if lib().orc_model_set_tensor(self.h, layer, ROLE[role], ptr(v), v.size) != 0:
+            raise ValueError(f"tensor {role} of layer {layer}: unknown role or {v.size} elements do not fit")
 
     def norm(self, layer: int, role: str) -> np.ndarray:
         n = lib().orc_model_norm(self.h, layer, ROLE[role], None)

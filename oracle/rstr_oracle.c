@@ -565,6 +565,7 @@ struct orc_model {
   uint64_t seed;
   layer_w* layers;
   qtensor head;      /* tied embedding, quantised */
+  float* embed;      /* f32 embedding of a host-tensor model (NULL: synthetic rows) */
   float* final_norm;
   float* rope_cos[2];
   float* rope_sin[2];
@@ -664,6 +665,7 @@ void orc_model_free(orc_model* m) {
   }
   free(m->layers);
   free_q(&m->head);
+  free(m->embed);
   free(m->final_norm);
   for (int i = 0; i < 2; i++) { free(m->rope_cos[i]); free(m->rope_sin[i]); }
   free(m);
@@ -716,6 +718,55 @@ int64_t orc_model_norm(const orc_model* m, int32_t layer, int32_t role, float* o
   return n;
 }
 
+/* Replace one tensor of a model by host f32 values (a checkpoint's tensors,  */
+/* widened to f32): linears and the tied embedding are quantised with the     */
+/* same block rules as the synthetic ones, norms are copied.  `n` must be the */
+/* tensor's element count.  Returns 0, or -1 for an unknown role or size.     */
+int32_t orc_model_set_tensor(orc_model* m, int32_t layer, int32_t role, const float* src, int64_t n) {
+  if (role == ORC_ROLE_EMBED) {
+    const int64_t want = (int64_t)m->d.vocab * m->d.d_model;
+    if (n != want) return -1;
+    if (!m->embed) m->embed = (float*)malloc(sizeof(float) * (size_t)want);
+    memcpy(m->embed, src, sizeof(float) * (size_t)want);
+  }
+  const qtensor* tc = find_linear(m, layer, role);
+  if (tc) {
+    qtensor* t = (qtensor*)tc;
+    if (n != (int64_t)t->n * t->k) return -1;
+    const int64_t nb = t->k / 32;
+    const int32_t bits = m->d.weight_bits;
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < t->n; r++)
+      for (int64_t b = 0; b < nb; b++) {
+        const float* w = src + (int64_t)r * t->k + 32 * b;
+        if (bits == 4)
+          quant_q4_block(w, (uint8_t*)t->wq + ((int64_t)r * nb + b) * 16, t->ws + (int64_t)r * nb + b);
+        else
+          quant_q8_block(w, (int8_t*)t->wq + ((int64_t)r * nb + b) * 32, t->ws + (int64_t)r * nb + b);
+      }
+    return 0;
+  }
+  float* g = NULL;
+  int64_t len = m->d.d_model;
+  if (role == ORC_ROLE_FINAL_NORM) {
+    g = m->final_norm;
+  } else if (layer >= 0 && layer < m->d.n_layers) {
+    layer_w* L = &m->layers[layer];
+    switch (role) {
+      case ORC_ROLE_ATTN_NORM: g = L->attn_norm; break;
+      case ORC_ROLE_FFN_PRE_NORM: g = L->ffn_pre_norm; break;
+      case ORC_ROLE_POST_ATTN_NORM: g = L->post_attn_norm; break;
+      case ORC_ROLE_FFN_POST_NORM: g = L->ffn_post_norm; break;
+      case ORC_ROLE_Q_NORM: g = L->q_norm; len = m->d.head_dim; break;
+      case ORC_ROLE_K_NORM: g = L->k_norm; len = m->d.head_dim; break;
+      default: break;
+    }
+  }
+  if (!g || n != len) return -1;
+  memcpy(g, src, sizeof(float) * (size_t)len);
+  return 0;
+}
+
 /* Embedding row prescaled in double (decoder_gpu.clj:80-91 prescaled-embed, */
 /* embed-row :500-505): (float)(sqrt(d) * (double)e) or e.                   */
 void orc_embed_row(const orc_model* m, int32_t token, float* out) {
@@ -723,7 +774,8 @@ void orc_embed_row(const orc_model* m, int32_t token, float* out) {
   uint64_t key = orc_tensor_key(m->seed, -1, ORC_ROLE_EMBED);
   double scale = m->d.embed_scale_sqrt_d ? sqrt((double)d) : 1.0;
   for (int32_t j = 0; j < d; j++) {
-    float e = orc_normal(key, (uint64_t)token * (uint64_t)d + (uint64_t)j, 0.0, 0.02);
+    float e = m->embed ? m->embed[(int64_t)token * d + j]
+                       : orc_normal(key, (uint64_t)token * (uint64_t)d + (uint64_t)j, 0.0, 0.02);
     out[j] = m->d.embed_scale_sqrt_d ? (float)(scale * (double)e) : e;
   }
 }

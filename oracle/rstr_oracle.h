@@ -96,6 +96,8 @@ typedef struct orc_decoder orc_decoder;
 
 orc_model* orc_model_synthetic(const orc_desc* desc, uint64_t seed);
 void orc_model_free(orc_model* m);
+/* Replace one tensor by host f32 values (linears/embedding quantised, norms copied). */
+int32_t orc_model_set_tensor(orc_model* m, int32_t layer, int32_t role, const float* src, int64_t n);
 /* Canonical packed bytes of one linear tensor (role, layer); returns bytes written. */
 int64_t orc_model_tensor(const orc_model* m, int32_t layer, int32_t role, void* wq, uint16_t* ws);
 /* f32 gain vector of a norm role; returns elements. */

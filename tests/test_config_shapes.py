@@ -54,7 +54,7 @@ def test_config2_shape_schedule_matches_oracle():
     steps = _replay(cfg, pl, batch, pages, maxpos, 32, 3)
     assert max(max(st["lengths"]) for st in steps) > 512  # windowed layers see a partial window
     # route pages are scattered over the physical pool, not lowest-first runs
-    pt = np.asarray(steps[-1]["page_table"])
+    pt = np.asarray(steps[-1]["page_table"]).reshape(batch, -1)
     first = pt[:, 0][pt[:, 0] >= 0]
     assert len(set(first.tolist())) == len(first) and first.max() > pages // 2
 

@@ -2,8 +2,14 @@
 properties ``test/pretrained/model_identity_test.clj`` checks), the worker's
 default measurements and option validation (``rstr.model_worker``), and on the
 GPU a worker opened from a checkpoint directory generating the same tokens as
-the same checkpoint bound and decoded by hand, with and without a bulk-prefill
-tile, then closing in order."""
+the CPU oracle decoding the same checkpoint (its tensors widened to f32 and
+quantised by the oracle), with and without a bulk-prefill tile, then closing
+in order.
+
+Fingerprint bytes are parity unpinned: the reference encodes the manifest with
+the ``boring`` archival format (model_identity.clj:62), which is absent here;
+this build hashes canonical JSON of the same manifest, so digests are stable and
+sensitive to the same fields but not byte-equal to the reference's."""
 import numpy as np
 import pytest
 
@@ -62,11 +68,14 @@ def test_default_measurements_and_validation():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("prefill_T", [None, 8])
-def test_worker_generates_like_the_hand_bound_checkpoint(tmp_path, prefill_T):
+def test_worker_generates_like_the_oracle_on_the_checkpoint(tmp_path, prefill_T):
     print("case worker", prefill_T, flush=True)
-    from rstr import hip, loader
+    import oracle as O
+    from rstr import loader
+    from rstr import safetensors as st
     from rstr.page_pool import PagePool
-    from rstr.paged_decoder import HipStepDevice, PagedDecoder
+    from rstr.paged_decoder import PagedDecoder
+    from test_config1 import OracleStepDevice
     from test_gpu_loader import _write_checkpoint
     _write_checkpoint(str(tmp_path), "llama")
     hf = loader.load_hf(str(tmp_path))
@@ -81,11 +90,21 @@ def test_worker_generates_like_the_hand_bound_checkpoint(tmp_path, prefill_T):
     finally:
         w.close()
         w.close()
-    with hip.Session(0) as sess:
-        m, cfg = loader.bind_hf(sess, str(tmp_path))
-        p = hip.Pool(m, 16, 16)
-        d = hip.Decoder(m, p, 1, 4, 64, 16)
-        pool = PagePool(16, 16, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"], "half", device=p)
-        want = PagedDecoder(pool, HipStepDevice(d), batch_size=1, maxpos=64, pages_per_sequence=4).generate(
-            "c", prompt, 9)
+    # the oracle decodes the same checkpoint: every tensor widened to f32
+    # (safetensors.clj:39-78) and quantised by the oracle's block rules
+    arch = loader.architecture(hf)
+    cfg = loader.model_config(hf, arch)
+    om = O.Model(cfg, seed=0)
+    try:
+        for layer, role, dtype, view in loader.raw_tensors(hf, arch):
+            om.set_tensor(layer, role, st.to_f32(view, dtype))
+        od = O.Decoder(om, 1, 16, 16, 4, 64, kv_f16=True, split=16)
+        try:
+            pool = PagePool(16, 16, cfg["n_layers"], cfg["n_kv"], cfg["head_dim"], "half", device=od)
+            want = PagedDecoder(pool, OracleStepDevice(od), batch_size=1, maxpos=64,
+                                pages_per_sequence=4).generate("c", prompt, 9)
+        finally:
+            od.close()
+    finally:
+        om.close()
     assert got == want and len(got) == 9

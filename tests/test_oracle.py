@@ -330,3 +330,50 @@ def test_argmax_reference_known_answer():
     logits = np.array([[1.0, 5.0, 5.0, 2.0], [9.0, np.nan, 8.0, np.nan]], np.float32)
     assert O.argmax_rows(logits).tolist() == [1, 1]
     assert O.argmax_rows(np.array([[-np.inf, -np.inf, -1.0]], np.float32)).tolist() == [2]
+
+
+def test_host_tensor_model_equals_the_synthetic_model():
+    """``Model.set_tensor`` (host f32 tensors: a checkpoint's) quantises and
+    stores exactly as the synthetic build does: a model whose every tensor is
+    set to the synthetic generator's f32 values equals the synthetic model in
+    packed weights, norms, embedding rows and a decode step's logits."""
+    from rstr import configs
+    cfg = configs.TINY_GEMMA
+    syn = O.Model(cfg, seed=4)
+    host = O.Model(cfg, seed=99)
+    try:
+        roles = ["q", "k", "v", "o", "gate", "up", "down", "attn_norm", "ffn_pre_norm", "q_norm", "k_norm",
+                 "post_attn_norm", "ffn_post_norm"]
+        for layer in list(range(cfg["n_layers"])) + [-1]:
+            for role in (roles if layer >= 0 else ["embed", "final_norm"]):
+                key = O.tensor_key(4, layer, O.ROLE[role])
+                if role.endswith("norm"):
+                    n = cfg["head_dim"] if role in ("q_norm", "k_norm") else cfg["d_model"]
+                    vals = O.normal(key, 0, n, 0.0 if cfg["gain_offset"] else 1.0, 0.02)
+                else:
+                    n, k = O.linear_shape(cfg, role)
+                    vals = O.normal(key, 0, n * k, 0.0, 0.02)
+                host.set_tensor(layer, role, vals)
+        with pytest.raises(ValueError):
+            host.set_tensor(0, "q", np.zeros(5, np.float32))
+        for layer in range(cfg["n_layers"]):
+            for role in ("q", "k", "v", "o", "gate", "up", "down"):
+                for a, b in zip(syn.tensor(layer, role), host.tensor(layer, role)):
+                    assert np.array_equal(a, b), (layer, role)
+            for role in roles[7:]:
+                assert np.array_equal(syn.norm(layer, role), host.norm(layer, role))
+        for a, b in zip(syn.tensor(-1, "embed"), host.tensor(-1, "embed")):
+            assert np.array_equal(a, b)
+        for tok in (0, 5, cfg["vocab"] - 1):
+            assert np.array_equal(syn.embed_row(tok), host.embed_row(tok))
+        outs = []
+        for m in (syn, host):
+            d = O.Decoder(m, 1, 16, 2, 2, 32, kv_f16=True, split=16)
+            d.prime_lanes([0], [9])
+            d.step_lanes([0], [0, 1], [0], [0, -1], [1], [0])
+            outs.append(d.logits())
+            d.close()
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    finally:
+        syn.close()
+        host.close()
