@@ -531,6 +531,7 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
     for _ in range(2):  # admissions of the steady-state start, first graph replays
         planner.plan_step()
     dev.step_seconds = dev.other_seconds = 0.0
+    dev.phase_ms.clear()
     host0 = planner.host_seconds
     times = []
     for _ in range(args.live_steps):
@@ -540,12 +541,32 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
     n = len(times)
     total = sum(times)
     step_s, other_s = dev.step_seconds, dev.other_seconds
+    phases = {k: round(v / n, 4) for k, v in dev.phase_ms.items()}
+    # idle probe: the last live step's descriptors again, back to back and with
+    # the host pausing as long as the planner did between calls; the device time
+    # of the same step graph tells the GPU's own ramp after idling apart from
+    # the library's host work
+    pause = max(0.0, (planner.host_seconds - host0 - step_s - other_s) / n)
+    probe = {}
+    for label, gap in (("back_to_back", 0.0), ("after_host_pause", pause)):
+        dev_ms = []
+        for _ in range(8):
+            if gap:
+                time.sleep(gap)
+            dec.step_lanes(**dev._desc)
+            dev_ms.append(dec.step_timing()["device_step"])
+        probe[label] = round(float(np.median(dev_ms)), 4)
+    probe["pause_ms"] = round(1e3 * pause, 3)
     return {"steps": n, "ms_per_step_median": round(1e3 * float(np.median(times)), 3),
             "ms_per_step_mean": round(1e3 * total / n, 3),
             "tokens_per_s_median": round(lanes / float(np.median(times)), 1) if lanes else None,
             "rstr_step_lanes_ms": round(1e3 * step_s / n, 3),
             "fills_copies_primes_ms": round(1e3 * other_s / n, 3),
-            "host_bookkeeping_ms": round(1e3 * ((planner.host_seconds - host0) - step_s - other_s) / n, 3)}
+            "host_bookkeeping_ms": round(1e3 * ((planner.host_seconds - host0) - step_s - other_s) / n, 3),
+            # inside rstr_step_lanes (rstr_decoder_step_timing), mean ms per call
+            "rstr_step_lanes_phases_ms": phases,
+            # the same step's device time (ms, median of 8) back to back and after a host pause
+            "idle_probe_device_step_ms": probe}
 
 
 def main():

@@ -205,6 +205,17 @@ int rstr_prime_rows(rstr_decoder* d, int32_t n, const int32_t* lanes, const floa
 int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int32_t* row_offsets,
                     const int32_t* positions, const int32_t* page_table, const int32_t* lengths,
                     const int32_t* start_positions, int32_t* tokens_out);
+/* No counterpart in the reference: a measurement helper for the serving
+ * loop's timing harness (continuation/benchmark.clj:180-194 times whole
+ * step-lanes! calls).  The phases of the decoder's last rstr_step_lanes call,
+ * in milliseconds: [0] descriptor validation, [1] wait for work queued before
+ * the call (fills, copies, primes), [2] descriptor packing into pinned
+ * staging, [3] enqueue (descriptor copy, step graph launch, token copy),
+ * [4] wait for the device, [5] token hand-back, [6] the whole call, [7] the
+ * device time of the step itself (HIP events around the step graph).  Writes
+ * min(n, RSTR_STEP_TIMING_FIELDS) values. */
+#define RSTR_STEP_TIMING_FIELDS 8
+int rstr_decoder_step_timing(rstr_decoder* d, double* out, int32_t n);
 /* Logits [batch][vocab] of the last step (decode-row! returning logits,
  * decoder_gpu.clj:1158-1170). */
 int rstr_decode_logits(rstr_decoder* d, float* logits_out);

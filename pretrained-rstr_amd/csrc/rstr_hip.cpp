@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -185,6 +186,9 @@ struct rstr_decoder {
   std::vector<StagedDev> sched;
   int64_t sched_desc_cap = 0, sched_pages_cap = 0, sched_tok_cap = 0;
   bool has_logits = false;
+  // phases of the last rstr_step_lanes call (rstr_decoder_step_timing)
+  hipEvent_t ev_step[2] = {nullptr, nullptr};
+  double step_ms[RSTR_STEP_TIMING_FIELDS] = {};
 };
 
 // ---------------------------------------------------------------------------
@@ -921,6 +925,8 @@ static void decoder_free(rstr_decoder* d) {
     if (q) hipFree(q);
   if (d->h_desc) hipHostFree(d->h_desc);
   if (d->h_tok) hipHostFree(d->h_tok);
+  for (hipEvent_t ev : d->ev_step)
+    if (ev) hipEventDestroy(ev);
   delete d;
 }
 
@@ -1000,6 +1006,8 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   A(dmalloc(&d->d_tokens, (size_t)batch));
   if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_desc, sizeof(int32_t) * d->desc_words);
   if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_tok, sizeof(int32_t) * batch);
+  for (hipEvent_t& ev : d->ev_step)
+    if (e == hipSuccess) e = hipEventCreate(&ev);
   if (e != hipSuccess) {
     decoder_free(d);
     return fail(s, RSTR_E_OOM, std::string("decoder allocation: ") + hipGetErrorString(e));
@@ -1361,19 +1369,42 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
   if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
   rstr_session* s = d->m->s;
   if (!d->head_tail) return fail(s, RSTR_E_STATE, "a bulk-prefill decoder has no head; use rstr_prefill_range");
+  using clk = std::chrono::steady_clock;
+  const auto t0 = clk::now();
   bool fused = false;
   int rc = validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions, &fused);
   if (rc) return rc;
   if (!tokens_out) return fail(s, RSTR_E_INVALID, "null token output");
+  const auto t1 = clk::now();
   HIPCHK(s, hipSetDevice(s->device));
   HIPCHK(s, hipStreamSynchronize(s->stream));
+  const auto t2 = clk::now();
   pack_desc(d, d->h_desc, slots, row_offsets, positions, page_table, lengths, start_positions);
+  const auto t3 = clk::now();
   HIPCHK(s, hipMemcpyAsync(d->desc, d->h_desc, sizeof(int32_t) * d->desc_words, hipMemcpyHostToDevice,
                            s->stream));
+  HIPCHK(s, hipEventRecord(d->ev_step[0], s->stream));
   if ((rc = run_step_device(d, fused))) return rc;
+  HIPCHK(s, hipEventRecord(d->ev_step[1], s->stream));
   HIPCHK(s, hipMemcpyAsync(d->h_tok, d->tokbuf, sizeof(int32_t) * d->B, hipMemcpyDeviceToHost, s->stream));
+  const auto t4 = clk::now();
   HIPCHK(s, hipStreamSynchronize(s->stream));
+  const auto t5 = clk::now();
   std::memcpy(tokens_out, d->h_tok, sizeof(int32_t) * d->B);
+  const auto t6 = clk::now();
+  auto ms = [](clk::time_point a, clk::time_point b) { return std::chrono::duration<double, std::milli>(b - a).count(); };
+  float dev = 0.0f;
+  HIPCHK(s, hipEventElapsedTime(&dev, d->ev_step[0], d->ev_step[1]));
+  const double v[RSTR_STEP_TIMING_FIELDS] = {ms(t0, t1), ms(t1, t2), ms(t2, t3), ms(t3, t4), ms(t4, t5), ms(t5, t6),
+                                             ms(t0, t6), (double)dev};
+  std::memcpy(d->step_ms, v, sizeof v);
+  return RSTR_OK;
+}
+
+extern "C" int rstr_decoder_step_timing(rstr_decoder* d, double* out, int32_t n) {
+  if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
+  if (!out || n < 0) return fail(d->m->s, RSTR_E_INVALID, "null timing output");
+  std::memcpy(out, d->step_ms, sizeof(double) * (size_t)std::min<int32_t>(n, RSTR_STEP_TIMING_FIELDS));
   return RSTR_OK;
 }
 

@@ -28,7 +28,8 @@ EXPORTS = (
     "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_chunk_export_submit",
     "rstr_chunk_restore_submit", "rstr_transfer_done", "rstr_transfer_complete", "rstr_chunk_bench", "rstr_decoder_open",
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
-    "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_prefill_open",
+    "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_decoder_step_timing",
+    "rstr_prefill_open",
     "rstr_prefill_range", "rstr_append_run", "rstr_tail_run",
     "rstr_attention_run", "rstr_attention_run_static",
     "rstr_attention_bench", "rstr_schedule_upload", "rstr_schedule_run",
@@ -119,6 +120,7 @@ def lib():
             "rstr_decode_logits": (i32, [P, P]),
             "rstr_decoder_read_rows": (i32, [P, P]),
             "rstr_decoder_set_graph": (i32, [P, i32]),
+            "rstr_decoder_step_timing": (i32, [P, P, i32]),
             "rstr_prefill_open": (i32, [P, P, i32, i32, i32, i32, C.POINTER(P)]),
             "rstr_prefill_range": (i32, [P, P, P, P, P, i32, i32]),
             "rstr_append_run": (i32, [P, i32, i32, P, P, P]),
@@ -445,6 +447,14 @@ class Decoder:
 
     def set_graph(self, enabled: bool):
         self.sess.check(lib().rstr_decoder_set_graph(self.h, 1 if enabled else 0))
+
+    STEP_TIMING = ("validate", "prior_sync", "pack", "enqueue", "device_wait", "handback", "call", "device_step")
+
+    def step_timing(self) -> dict:
+        """Phases (ms) of the last step_lanes call (rstr_decoder_step_timing)."""
+        out = np.zeros(len(self.STEP_TIMING), np.float64)
+        self.sess.check(lib().rstr_decoder_step_timing(self.h, _p(out), out.size))
+        return dict(zip(self.STEP_TIMING, out.tolist()))
 
     def prime_lanes(self, lanes, tokens):
         lanes, tokens = _i32(lanes), _i32(tokens)

@@ -69,6 +69,7 @@ class LiveDevice:
         self.cur = None
         self.step_seconds = 0.0
         self.other_seconds = 0.0
+        self.phase_ms = collections.Counter()  # summed rstr_step_lanes phases
 
     def begin(self):
         self.cur = {"fill_pages": [], "cow_pairs": [], "prime_lanes": [], "prime_tokens": []}
@@ -102,6 +103,7 @@ class LiveDevice:
         t0 = time.perf_counter()
         self._tokens = self.decoder.step_lanes(**self._desc)
         self.step_seconds += time.perf_counter() - t0
+        self.phase_ms.update(self.decoder.step_timing())
 
     def download_tokens(self):
         return self._tokens
