@@ -253,6 +253,20 @@ int rstr_prefill_range(rstr_decoder* d, const int32_t* tokens, const int32_t* sl
 int rstr_append_run(rstr_pool* p, int32_t layer, int32_t batch, const float* k_rows,
                     const float* v_rows, const int32_t* slots);
 
+/* ---- isolated dequantising linear ------------------------------------------------
+ * Replaces qlinear-i8 over one resident weight (decoder.clj:206-213; the GPU
+ * call sites qmatmul-q4k-dp4a-rows!, decoder_gpu.clj:170-194) as a
+ * kernel-level check: y[rows][n] = x W^T for int8 activations
+ * xq[rows][k] with per-32-block scales xs[rows][k/32] (4-bit significands, as
+ * the step's quantiser writes them), through one projection form -- 0 the
+ * step's own choice, 1 the MFMA tile, 2 the one-wave weight-streaming GEMV, 3
+ * its workgroup form (2 and 3 take rows <= 4) -- with the K range in `splits`
+ * slices combined in the consumers' canonical tree.  Roles: RSTR_ROLE_EMBED
+ * (the tied head), RSTR_ROLE_Q (the fused [q|k|v] tensor), RSTR_ROLE_O,
+ * RSTR_ROLE_GATE (the fused [gate|up] tensor), RSTR_ROLE_DOWN. */
+int rstr_linear_run(rstr_model* m, int32_t layer, int32_t role, int32_t rows, const int8_t* xq,
+                    const float* xs, int32_t splits, int32_t form, float* y);
+
 /* ---- isolated decode tail ------------------------------------------------------
  * Replaces decode-tail! (decoder_gpu.clj:73-78; KAT
  * decoder_gpu_composition_test.clj:9-20) with the decode step's own tail

@@ -62,6 +62,13 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 bool qgemm_act_fused(int ff, int mpad);
 hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, int ff, int geglu,
                             ActBuf& out);
+// The same projection with the kernel form chosen by the caller (kernel-level
+// parity tests): AUTO is launch_qgemm's own choice; TILE the MFMA tile plan;
+// WAVE_GEMV / WG_GEMV the weight-streaming GEMVs (m_rows <= 4).  A form that
+// does not serve the shape returns hipErrorInvalidValue before any device work.
+enum { QG_FORM_AUTO = 0, QG_FORM_TILE = 1, QG_FORM_WAVE_GEMV = 2, QG_FORM_WG_GEMV = 3 };
+hipError_t launch_qgemm_form(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                             int splits, size_t slice_stride, int form);
 // Few-row weight-streaming GEMVs (m_rows <= 4; launch_qgemm picks them per
 // shape): one wave per (column tile, split), or one workgroup per (column
 // tile, split) whose waves share the split's 4-block groups.

@@ -1018,11 +1018,14 @@ static void qg_dispatch_t(const QgLaunch& a, const QgPlan& p) {
   else qg_dispatch_q<1, 1, B>(a, p.nq);
 }
 
-hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y,
-                        int ldy, int splits, size_t slice_stride) {
+hipError_t launch_qgemm_form(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                             int splits, size_t slice_stride, int form) {
   const int nb = w.k / 32;
   if (w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4)) return hipErrorInvalidValue;
   if (w.bits != 4 && w.bits != 8) return hipErrorInvalidValue;
+  if (form == QG_FORM_WAVE_GEMV) return launch_qgemv(st, w, x, m_rows, y, ldy, splits, slice_stride);
+  if (form == QG_FORM_WG_GEMV) return launch_qgemv_wg(st, w, x, m_rows, y, ldy, splits, slice_stride);
+  if (form != QG_FORM_AUTO && form != QG_FORM_TILE) return hipErrorInvalidValue;
   // Few rows: the weight-streaming GEMVs.  Measured on MI355X (weights streamed
   // from HBM, four K slices; us for the GEMV forms against the 16-row MFMA
   // tile): one row against a long K (the MLP down projection, 4096 x 14336)
@@ -1035,7 +1038,7 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   // only on matrices up to 4M weights (Qwen3-0.6B down 4.3 vs 4.8).  Quarters
   // that are not whole 4-block groups (K = 640: Gemma-3-270M) stay on the tile,
   // whose preloaded chains were faster there (config1 0.750 vs 0.760 ms/step).
-  if (x.mpad == 16 && m_rows <= 4) {
+  if (form == QG_FORM_AUTO && x.mpad == 16 && m_rows <= 4) {
     if (m_rows == 1 && w.k >= 8192) {
       if (launch_qgemv(st, w, x, m_rows, y, ldy, splits, slice_stride) == hipSuccess) return hipSuccess;
     } else if (splits == 4 && (nb / 4) % 4 == 0 &&
@@ -1067,6 +1070,11 @@ hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m
   if (w.bits == 4) qg_dispatch_t<4>(L, p);
   else qg_dispatch_t<8>(L, p);
   return hipGetLastError();
+}
+
+hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy, int splits,
+                        size_t slice_stride) {
+  return launch_qgemm_form(st, w, x, m_rows, y, ldy, splits, slice_stride, QG_FORM_AUTO);
 }
 
 // Gate/up with the gated activation fused (k_qgemm<4, 1, BITS, 4, KC, NT, true>):

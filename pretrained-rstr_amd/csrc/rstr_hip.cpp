@@ -1690,6 +1690,72 @@ extern "C" int rstr_tail_run(rstr_session* s, int32_t rows, int32_t vocab, int32
 }
 
 // ---------------------------------------------------------------------------
+// isolated dequantising linear (kernel-level parity of every projection form)
+// ---------------------------------------------------------------------------
+extern "C" int rstr_linear_run(rstr_model* m, int32_t layer, int32_t role, int32_t rows, const int8_t* xq,
+                               const float* xs, int32_t splits, int32_t form, float* y) {
+  if (!m) return fail(nullptr, RSTR_E_INVALID, "null model");
+  rstr_session* s = m->s;
+  if (!xq || !xs || !y) return fail(s, RSTR_E_INVALID, "null linear buffer");
+  const QTensor* t = nullptr;
+  if (role == RSTR_ROLE_EMBED) t = &m->head;
+  else if (layer >= 0 && layer < (int32_t)m->layers.size()) {
+    LayerW& L = m->layers[layer];
+    if (role == RSTR_ROLE_Q) t = &L.qkv;
+    else if (role == RSTR_ROLE_O) t = &L.o;
+    else if (role == RSTR_ROLE_GATE) t = &L.gu;
+    else if (role == RSTR_ROLE_DOWN) t = &L.down;
+  }
+  if (!t) return fail(s, RSTR_E_INVALID, "no such linear (roles: embed, q = fused qkv, o, gate = fused gate/up, down)");
+  if (rows < 1 || rows > 4096) return fail(s, RSTR_E_INVALID, "rows must be in [1, 4096]");
+  if (splits != 1 && splits != 2 && splits != 4) return fail(s, RSTR_E_INVALID, "splits must be 1, 2 or 4");
+  if (form < QG_FORM_AUTO || form > QG_FORM_WG_GEMV) return fail(s, RSTR_E_INVALID, "unknown projection form");
+  const int K = t->k, N = t->n, nb = K / 32, mpad = (rows + 15) / 16 * 16;
+  // activation operand in the MFMA tile order: fp16 q*d [mpad/16][nb][g][m%16][8]
+  // (exact: d has a 4-bit significand), scales [nb][mpad]; padding rows are 0
+  std::vector<_Float16> hq((size_t)mpad * K, (_Float16)0.0f);
+  std::vector<float> hs((size_t)nb * mpad, 0.0f);
+  for (int r = 0; r < rows; r++)
+    for (int b = 0; b < nb; b++) {
+      const float d = xs[(size_t)r * nb + b];
+      hs[(size_t)b * mpad + r] = d;
+      for (int g = 0; g < 4; g++)
+        for (int e = 0; e < 8; e++)
+          hq[((((size_t)(r >> 4) * nb + b) * 4 + g) * 16 + (r & 15)) * 8 + e] =
+              (_Float16)((float)xq[(size_t)r * K + 32 * b + 8 * g + e] * d);
+    }
+  HIPCHK(s, hipSetDevice(s->device));
+  ActBuf x;
+  x.mpad = mpad;
+  float* dy = nullptr;
+  hipError_t e = dmalloc(&x.q, hq.size());
+  if (e == hipSuccess) e = dmalloc(&x.s, hs.size());
+  if (e == hipSuccess) e = dmalloc(&dy, (size_t)splits * rows * N);
+  if (e == hipSuccess) e = hipMemcpy(x.q, hq.data(), hq.size() * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(x.s, hs.data(), hs.size() * 4, hipMemcpyHostToDevice);
+  hipError_t le = hipSuccess;
+  if (e == hipSuccess) {
+    le = launch_qgemm_form(s->stream, *t, x, rows, dy, N, splits, (size_t)rows * N, form);
+    if (le == hipSuccess) e = hipStreamSynchronize(s->stream);
+  }
+  std::vector<float> sl((size_t)splits * rows * N);
+  if (e == hipSuccess && le == hipSuccess) e = hipMemcpy(sl.data(), dy, sl.size() * 4, hipMemcpyDeviceToHost);
+  for (void* q : {(void*)x.q, (void*)x.s, (void*)dy})
+    if (q) hipFree(q);
+  if (le == hipErrorInvalidValue) return fail(s, RSTR_E_INVALID, "the projection form does not serve this shape");
+  HIPCHK(s, le);
+  HIPCHK(s, e);
+  // slices in the consumers' canonical tree: (s0 + s1) or ((s0 + s1) + (s2 + s3))
+  const size_t n = (size_t)rows * N;
+  for (size_t i = 0; i < n; i++) {
+    if (splits == 1) y[i] = sl[i];
+    else if (splits == 2) y[i] = sl[i] + sl[n + i];
+    else y[i] = (sl[i] + sl[n + i]) + (sl[2 * n + i] + sl[3 * n + i]);
+  }
+  return RSTR_OK;
+}
+
+// ---------------------------------------------------------------------------
 // isolated routed attention
 // ---------------------------------------------------------------------------
 struct AttnBufs {

@@ -30,7 +30,7 @@ EXPORTS = (
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
     "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_decoder_step_timing",
     "rstr_prefill_open",
-    "rstr_prefill_range", "rstr_append_run", "rstr_tail_run",
+    "rstr_prefill_range", "rstr_append_run", "rstr_tail_run", "rstr_linear_run",
     "rstr_attention_run", "rstr_attention_run_static",
     "rstr_attention_bench", "rstr_schedule_upload", "rstr_schedule_run",
     "rstr_decoder_profile_steps",
@@ -121,6 +121,7 @@ def lib():
             "rstr_decoder_read_rows": (i32, [P, P]),
             "rstr_decoder_set_graph": (i32, [P, i32]),
             "rstr_decoder_step_timing": (i32, [P, P, i32]),
+            "rstr_linear_run": (i32, [P, i32, i32, i32, P, P, i32, i32, P]),
             "rstr_prefill_open": (i32, [P, P, i32, i32, i32, i32, C.POINTER(P)]),
             "rstr_prefill_range": (i32, [P, P, P, P, P, i32, i32]),
             "rstr_append_run": (i32, [P, i32, i32, P, P, P]),
@@ -255,6 +256,22 @@ class Model:
     @property
     def weight_bytes(self) -> int:
         return int(lib().rstr_model_weight_bytes(self.h))
+
+    LINEAR_FORMS = {"auto": 0, "tile": 1, "wave_gemv": 2, "wg_gemv": 3}
+
+    def linear(self, layer: int, role: str, xq, xs, splits: int, form: str = "auto") -> np.ndarray:
+        """One resident projection on int8 activations (rstr_linear_run): role
+        "q" is the fused [q|k|v] tensor, "gate" the fused [gate|up] one, "embed"
+        the tied head."""
+        xq = np.ascontiguousarray(np.asarray(xq, np.int8))
+        xs = np.ascontiguousarray(np.asarray(xs, np.float32))
+        rows, k = xq.shape
+        n = {"q": (self.cfg["n_q"] + 2 * self.cfg["n_kv"]) * self.cfg["head_dim"], "o": self.cfg["d_model"],
+             "gate": 2 * self.cfg["d_ff"], "down": self.cfg["d_model"], "embed": self.cfg["vocab"]}[role]
+        y = np.empty((rows, n), np.float32)
+        self.sess.check(lib().rstr_linear_run(self.h, layer, ROLE[role], rows, _p(xq), _p(xs), splits,
+                                              self.LINEAR_FORMS[form], _p(y)))
+        return y
 
     def export_linear(self, layer: int, role: str):
         cfg = self.cfg

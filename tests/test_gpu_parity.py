@@ -808,3 +808,52 @@ def test_activation_scale_clamp_regimes_match_the_oracle(sess):
     pa = _clamp_case(sess, 65504.0, plain=True, hip_side=False)
     pb = _clamp_case(sess, 64512.0, plain=True, hip_side=False)
     assert not np.array_equal(pa["oracle"][1][0], pb["oracle"][1][0])
+
+
+# ---------------------------------------------------------------------------
+# every projection form at every row count and K-slice count
+# ---------------------------------------------------------------------------
+LINEAR_CFG = configs._desc(n_layers=1, d_model=4096, d_ff=14336, n_q=32, n_kv=8, head_dim=128, vocab=2048,
+                           eps=1e-5, rope_global=500000.0, rope_local=500000.0)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_projection_forms_rows_and_slices_match_the_oracle(sess, bits):
+    """rstr_linear_run at Llama-3-8B widths (qkv 6144x4096, o 4096x4096, gate/up
+    28672x4096, down 4096x14336): the MFMA tile at 1..4, 16, 64 and 128 rows, the
+    one-wave weight-streaming GEMV and its workgroup form at 1..4 rows, each at 1, 2
+    and 4 K slices where the form serves the shape, bit for bit against the
+    oracle's canonical linear.  Includes the GEMV at two rows with all four K
+    quarters in one wave (one slice), the instantiation once seen to lose a
+    quarter's partial in a since-replaced chain."""
+    cfg = configs.with_bits(LINEAR_CFG, bits)
+    print(f"case projection forms q{bits}", flush=True)
+    om = O.Model(cfg, seed=7)
+    m = hip.Model(sess, cfg, seed=7)
+    rng = np.random.default_rng(bits)
+    ran = 0
+    try:
+        weights = {"q": [om.tensor(0, r) for r in ("q", "k", "v")], "o": [om.tensor(0, "o")],
+                   "gate": [om.tensor(0, r) for r in ("gate", "up")], "down": [om.tensor(0, "down")]}
+        for role, parts in weights.items():
+            wq = np.concatenate([p[0] for p in parts])
+            ws = np.concatenate([p[1] for p in parts])
+            k = wq.shape[1] * 32
+            for rows in (1, 2, 3, 4, 16, 64, 128):
+                x = (rng.standard_normal((rows, k)) * rng.uniform(0.1, 3.0, (rows, 1))).astype(np.float32)
+                xq, xs = O.quant_act(x)
+                want = O.qlinear(bits, wq, ws, xq, xs)
+                forms = ("tile",) if rows > 4 else ("tile", "wave_gemv", "wg_gemv")
+                for form in forms:
+                    for splits in (1, 2, 4):
+                        try:
+                            got = m.linear(0, role, xq, xs, splits, form)
+                        except hip.RstrError as e:
+                            assert "does not serve" in str(e), e
+                            continue
+                        ran += 1
+                        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (role, rows, form, splits)
+        assert ran > 120
+    finally:
+        m.close()
+        om.close()
