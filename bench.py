@@ -101,7 +101,7 @@ def _attention_workload(args, sess) -> dict:
                    "lanes": B, "page_size": ps, "physical_pages": physical, "attention_split": args.split,
                    "mean_ctx": round(float(lengths.mean()), 1), "parallelism": "1 GPU (replica)"},
         "roofline": {"bound": "hbm", "achieved": round(ugbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ugbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(ugbs / HBM_PEAK_GBS, 4), "traffic": attn_traffic(args.workload),
                      "kernel": "k_attn_split (unique KV bytes per launch)", "bytes_per_launch": unique,
                      "avg_launch_ms": round(split_ms, 4)},
         "logical_bytes_per_launch": logical, "merge_ms": round(merge_ms, 4),
@@ -445,6 +445,15 @@ def cpu_attention_baseline(q, lengths, ps, n_kv, hd, scale, split, budget_s) -> 
             "sample": f"{n} of {len(lengths)} lanes ({int(sub.sum())} of {total} tokens), {reps} launches"}
 
 
+def attn_traffic(workload_name):
+    """HBM bytes per k_attn_split launch from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE runs of this workload (profiles/attn_split_<workload>_traffic.json), or None."""
+    tfile = os.path.join(ROOT, "profiles", f"attn_split_{workload_name}_traffic.json")
+    if os.path.exists(tfile):
+        return json.load(open(tfile)).get("hbm_bytes_per_launch")
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -731,10 +740,7 @@ def _decode_workload(args, sess) -> dict:
     classes = class_rates(cfg, prof, args.profile_steps, prof_plan, model.weight_bytes)
     dominant = max(("qgemm", "head", "attn_split"), key=lambda k: classes[k]["ms_per_step"])
     if dominant == "attn_split":
-        traffic = None
-        tfile = os.path.join(ROOT, "profiles", f"attn_split_{args.workload}_traffic.json")
-        if os.path.exists(tfile):
-            traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+        traffic = attn_traffic(args.workload)
         roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "kernel": "k_attn_split (paged attention, per layer launch)",
