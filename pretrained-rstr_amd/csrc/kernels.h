@@ -69,6 +69,21 @@ hipError_t launch_qgemm_act(hipStream_t st, const QTensor& w, const ActBuf& x, i
 enum { QG_FORM_AUTO = 0, QG_FORM_TILE = 1, QG_FORM_WAVE_GEMV = 2, QG_FORM_WG_GEMV = 3 };
 hipError_t launch_qgemm_form(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
                              int splits, size_t slice_stride, int form);
+// The down projection with its input computed in the projection itself: at
+// one to four rows, where launch_qgemm runs a weight-streaming GEMV, the
+// activation gate (launch_act_quant) folds into the GEMV's staging of its
+// activations -- hh = act(gate) * up from the gate/up slices of the
+// workgroup's K range, its 32-block scale and integers by the rule of
+// launch_act_quant, so the bits equal launch_act_quant followed by
+// launch_qgemm.  Returns hipErrorNotSupported, before any device work, for any
+// other shape (the caller then launches the two kernels).
+struct ActIn {
+  const float* gu;   // gate/up output slices [S][rows][2*ff] (gate | up)
+  size_t stride;     // floats between slices
+  int S, ff, geglu;
+};
+hipError_t launch_qgemm_actin(hipStream_t st, const QTensor& w, const ActIn& ain, int mpad, int m_rows, float* y,
+                              int ldy, int splits, size_t slice_stride);
 // Few-row weight-streaming GEMVs (m_rows <= 4; launch_qgemm picks them per
 // shape): one wave per (column tile, split), or one workgroup per (column
 // tile, split) whose waves share the split's 4-block groups.

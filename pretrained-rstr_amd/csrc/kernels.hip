@@ -193,6 +193,60 @@ __device__ __forceinline__ h8 unpack_q8(uint32_t x0, uint32_t x1, uint32_t E) {
   return r;
 }
 
+// hh = act(gate) * up for the 8 consecutive inputs k0..k0+7 of row m of the
+// down projection, from the gate/up slices added in the canonical tree (the
+// arithmetic of k_act_quant); rows past m_rows give 0.
+__device__ __forceinline__ void act_in_row8(const ActIn& a, int m, int m_rows, int k0, float hh[8]) {
+  if (m >= m_rows) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) hh[e] = 0.0f;
+    return;
+  }
+  const size_t r = (size_t)m * 2 * a.ff + k0;
+  f4 g[4][2], u[4][2];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int sk = k < a.S ? k : 0;
+    const float* p = a.gu + sk * a.stride + r;
+    g[k][0] = *reinterpret_cast<const f4*>(p);
+    g[k][1] = *reinterpret_cast<const f4*>(p + 4);
+    u[k][0] = *reinterpret_cast<const f4*>(p + a.ff);
+    u[k][1] = *reinterpret_cast<const f4*>(p + a.ff + 4);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    f4 gv, uv;
+    if (a.S == 1) { gv = g[0][h]; uv = u[0][h]; }
+    else if (a.S == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) { gv[i] = g[0][h][i] + g[1][h][i]; uv[i] = u[0][h][i] + u[1][h][i]; }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        gv[i] = (g[0][h][i] + g[1][h][i]) + (g[2][h][i] + g[3][h][i]);
+        uv[i] = (u[0][h][i] + u[1][h][i]) + (u[2][h][i] + u[3][h][i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) hh[4 * h + i] = (a.geglu ? dgelu(gv[i]) : dsilu(gv[i])) * uv[i];
+  }
+}
+
+// |max| over the 8 values of one lane (the caller reduces across the lanes of
+// the 32-block), then the quantised integers of a block scale d by the rule of
+// quant_store: q = rint(hh / d) clamped to +-127.
+__device__ __forceinline__ float amax8(const float hh[8]) {
+  float a = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) a = fmaxf(a, fabsf(hh[e]));
+  return a;
+}
+__device__ __forceinline__ void quant8(const float hh[8], float d, float q[8]) {
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) q[e] = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(hh[e] * id)));
+}
+
 // Workgroup: 4 waves over the same RT row tiles (RT*16 rows) and K range, wave
 // w owning column tiles (4*blockIdx.x + w)*CT ..+CT-1.  The K range is NQ whole
 // quarters (split s of 4/NQ); with NQ < 4 the workgroups of one column block
@@ -550,11 +604,11 @@ __device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
 }
 
-template <int M, int BITS, int NQ, int GD, int WV>
+template <int M, int BITS, int NQ, int GD, int WV, bool AIN = false>
 __global__ __launch_bounds__(64 * WV) void k_qgemv(const uint32_t* __restrict__ W, const uint16_t* __restrict__ Ws,
                                               const _Float16* __restrict__ X, const float* __restrict__ Xs,
                                               int nb, int mpad, float* __restrict__ Y, int ldy, int m_rows,
-                                              size_t slice_stride) {
+                                              size_t slice_stride, ActIn ain) {
   constexpr int DW = BITS == 4 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -597,14 +651,31 @@ __global__ __launch_bounds__(64 * WV) void k_qgemv(const uint32_t* __restrict__ 
     const int p = p0 + tid;
     const int pc = min(p, npair * 4 - 1);
     const int g = pc & 3, pr = pc >> 2, m = pr % M, b = b_begin + pr / M;
-    const h8 xv = *reinterpret_cast<const h8*>(X + ((size_t)(b * 4 + g) * 16 + m) * 8);
-    const float d = Xs[(size_t)b * mpad + m];
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
     int q[8], qsum = 0;
+    float d;
+    if constexpr (AIN) {
+      // the gate's activation computed here: a quad of lanes holds one 32-block
+      float hh[8], qf[8];
+      act_in_row8(ain, m, m_rows, 32 * b + 8 * g, hh);
+      float a = amax8(hh);
+      a = fmaxf(a, xor_lane<1>(a));
+      a = fmaxf(a, xor_lane<2>(a));
+      d = act_scale(a);
+      quant8(hh, d, qf);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      q[e] = (int)__builtin_rintf((float)xv[e] * id);
-      qsum += q[e];
+      for (int e = 0; e < 8; e++) {
+        q[e] = (int)qf[e];
+        qsum += q[e];
+      }
+    } else {
+      const h8 xv = *reinterpret_cast<const h8*>(X + ((size_t)(b * 4 + g) * 16 + m) * 8);
+      d = Xs[(size_t)b * mpad + m];
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        q[e] = (int)__builtin_rintf((float)xv[e] * id);
+        qsum += q[e];
+      }
     }
     qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, true);  // quad xor 1
     qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, true);  // quad xor 2
@@ -692,8 +763,10 @@ __global__ __launch_bounds__(64 * WV) void k_qgemv(const uint32_t* __restrict__ 
 
 // GEMV launch for m_rows <= 4 (rows of the first 16-row tile).  Returns
 // hipErrorInvalidValue, before any device work, for a shape it does not serve.
-hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
-                        int splits, size_t slice_stride) {
+namespace {
+template <bool AIN_>
+hipError_t qgemv_go(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy, int splits,
+                    size_t slice_stride, const ActIn& ain) {
   const int nb = w.k / 32;
   if (m_rows < 1 || m_rows > 4 || w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4))
     return hipErrorInvalidValue;
@@ -708,11 +781,11 @@ hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 #define RSTR_GV(M_, B_, Q_)                                                                                  \
   do {                                                                                                       \
     if (WVN == 4)                                                                                            \
-      hipLaunchKernelGGL((k_qgemv<M_, B_, Q_, 8, 4>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
-                         ldy, m_rows, slice_stride);                                                         \
+      hipLaunchKernelGGL((k_qgemv<M_, B_, Q_, 8, 4, AIN_>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, \
+                         y, ldy, m_rows, slice_stride, ain);                                                 \
     else                                                                                                     \
-      hipLaunchKernelGGL((k_qgemv<M_, B_, Q_, 8, 1>), grid, dim3(64), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y,  \
-                         ldy, m_rows, slice_stride);                                                         \
+      hipLaunchKernelGGL((k_qgemv<M_, B_, Q_, 8, 1, AIN_>), grid, dim3(64), lds, st, W, w.s, x.q, x.s, nb, x.mpad, \
+                         y, ldy, m_rows, slice_stride, ain);                                                 \
   } while (0)
 #define RSTR_GV_Q(M_, B_)                    \
   do {                                       \
@@ -734,17 +807,23 @@ hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m
 #undef RSTR_GV
   return hipGetLastError();
 }
+}  // namespace
+
+hipError_t launch_qgemv(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                        int splits, size_t slice_stride) {
+  return qgemv_go<false>(st, w, x, m_rows, y, ldy, splits, slice_stride, ActIn{});
+}
 
 // Workgroup form of the GEMV: one workgroup per (column tile, split) whose four
 // waves take the split's 4-block groups round robin (wave w: groups w, w+4, ...),
 // so up to 4*GD groups of one column tile are in flight at once; block dots and
 // scales meet in LDS, and the quarter chains run one wave per quarter before
 // wave 0 adds them in the canonical tree.  Same arithmetic as k_qgemv.
-template <int M, int BITS, int NQ, int GD>
+template <int M, int BITS, int NQ, int GD, bool AIN = false>
 __global__ __launch_bounds__(256) void k_qgemv_wg(const uint32_t* __restrict__ W, const uint16_t* __restrict__ Ws,
                                                  const _Float16* __restrict__ X, const float* __restrict__ Xs,
                                                  int nb, int mpad, float* __restrict__ Y, int ldy, int m_rows,
-                                                 size_t slice_stride) {
+                                                 size_t slice_stride, ActIn ain) {
   constexpr int DW = BITS == 4 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -788,14 +867,31 @@ __global__ __launch_bounds__(256) void k_qgemv_wg(const uint32_t* __restrict__ W
     const int p = p0 + tid;
     const int pc = min(p, npair * 4 - 1);
     const int g = pc & 3, pr = pc >> 2, m = pr % M, b = b_begin + pr / M;
-    const h8 xv = *reinterpret_cast<const h8*>(X + ((size_t)(b * 4 + g) * 16 + m) * 8);
-    const float d = Xs[(size_t)b * mpad + m];
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
     int q[8], qsum = 0;
+    float d;
+    if constexpr (AIN) {
+      // the gate's activation computed here: a quad of lanes holds one 32-block
+      float hh[8], qf[8];
+      act_in_row8(ain, m, m_rows, 32 * b + 8 * g, hh);
+      float a = amax8(hh);
+      a = fmaxf(a, xor_lane<1>(a));
+      a = fmaxf(a, xor_lane<2>(a));
+      d = act_scale(a);
+      quant8(hh, d, qf);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      q[e] = (int)__builtin_rintf((float)xv[e] * id);
-      qsum += q[e];
+      for (int e = 0; e < 8; e++) {
+        q[e] = (int)qf[e];
+        qsum += q[e];
+      }
+    } else {
+      const h8 xv = *reinterpret_cast<const h8*>(X + ((size_t)(b * 4 + g) * 16 + m) * 8);
+      d = Xs[(size_t)b * mpad + m];
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        q[e] = (int)__builtin_rintf((float)xv[e] * id);
+        qsum += q[e];
+      }
     }
     qsum += __builtin_amdgcn_update_dpp(0, qsum, 0xB1, 0xF, 0xF, true);  // quad xor 1
     qsum += __builtin_amdgcn_update_dpp(0, qsum, 0x4E, 0xF, 0xF, true);  // quad xor 2
@@ -880,8 +976,10 @@ __global__ __launch_bounds__(256) void k_qgemv_wg(const uint32_t* __restrict__ W
   }
 }
 
-hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
-                           int splits, size_t slice_stride) {
+namespace {
+template <bool AIN_>
+hipError_t qgemv_wg_go(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy, int splits,
+                       size_t slice_stride, const ActIn& ain) {
   const int nb = w.k / 32;
   if (m_rows < 1 || m_rows > 4 || w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4))
     return hipErrorInvalidValue;
@@ -895,11 +993,11 @@ hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, in
 #define RSTR_GV(M_, B_, Q_)                                                                                   \
   do {                                                                                                        \
     if (ngroups <= 8)                                                                                         \
-      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 2>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
-                         ldy, m_rows, slice_stride);                                                          \
+      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 2, AIN_>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, \
+                         x.mpad, y, ldy, m_rows, slice_stride, ain);                                          \
     else                                                                                                      \
-      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 8>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, x.mpad, y, \
-                         ldy, m_rows, slice_stride);                                                          \
+      hipLaunchKernelGGL((k_qgemv_wg<M_, B_, Q_, 8, AIN_>), grid, dim3(256), lds, st, W, w.s, x.q, x.s, nb, \
+                         x.mpad, y, ldy, m_rows, slice_stride, ain);                                          \
   } while (0)
 #define RSTR_GV_Q(M_, B_)                    \
   do {                                       \
@@ -920,6 +1018,12 @@ hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, in
 #undef RSTR_GV_Q
 #undef RSTR_GV
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_qgemv_wg(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy,
+                           int splits, size_t slice_stride) {
+  return qgemv_wg_go<false>(st, w, x, m_rows, y, ldy, splits, slice_stride, ActIn{});
 }
 
 namespace {
@@ -1075,6 +1179,36 @@ hipError_t launch_qgemm_form(hipStream_t st, const QTensor& w, const ActBuf& x, 
 hipError_t launch_qgemm(hipStream_t st, const QTensor& w, const ActBuf& x, int m_rows, float* y, int ldy, int splits,
                         size_t slice_stride) {
   return launch_qgemm_form(st, w, x, m_rows, y, ldy, splits, slice_stride, QG_FORM_AUTO);
+}
+
+// Down projection at one to four rows with act(gate)*up computed while the
+// GEMV stages its activations (the separate activation launch and its
+// quantised buffer drop out of the step).  Served where launch_qgemm would run
+// k_qgemv or k_qgemv_wg, with the same arithmetic; anything else returns
+// hipErrorNotSupported before any device work, and the caller runs
+// launch_act_quant + launch_qgemm instead.  Measured on MI355X: config1 (Gemma-3
+// 270M, one lane) 0.737 -> 0.725 ms/step, the one-lane Llama-3-8B step unchanged
+// (2.29 ms).  The same staging in the preloaded 16-row MFMA tile made config2
+// slower (0.79 -> 0.98 ms/step): 40 workgroups each rebuilt a quarter of the
+// activation for all 16 rows from four slices, so it is not used there.
+hipError_t launch_qgemm_actin(hipStream_t st, const QTensor& w, const ActIn& ain, int mpad, int m_rows, float* y,
+                              int ldy, int splits, size_t slice_stride) {
+  const int nb = w.k / 32;
+  if (mpad != 16 || m_rows < 1 || m_rows > 16 || w.k != ain.ff || !ain.gu || (ain.S != 1 && ain.S != 2 && ain.S != 4))
+    return hipErrorNotSupported;
+  if (w.n % 16 || nb % 4 || (splits != 1 && splits != 2 && splits != 4) || (w.bits != 4 && w.bits != 8))
+    return hipErrorNotSupported;
+  ActBuf x{};
+  x.mpad = mpad;
+  if (m_rows <= 4) {
+    if (m_rows == 1 && w.k >= 8192) {
+      if (qgemv_go<true>(st, w, x, m_rows, y, ldy, splits, slice_stride, ain) == hipSuccess) return hipSuccess;
+    } else if (splits == 4 && (nb / 4) % 4 == 0 &&
+               (m_rows <= 2 || (size_t)w.n * (size_t)w.k <= ((size_t)4 << 20))) {
+      if (qgemv_wg_go<true>(st, w, x, m_rows, y, ldy, splits, slice_stride, ain) == hipSuccess) return hipSuccess;
+    }
+  }
+  return hipErrorNotSupported;
 }
 
 // Gate/up with the gated activation fused (k_qgemm<4, 1, BITS, 4, KC, NT, true>):

@@ -1316,10 +1316,21 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool
       run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act_ff, B, d->o, dm, d->s_down, sd); });
     } else {
       run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.gu, d->act, B, d->gu, 2 * md.d_ff, d->s_gu, sg); });
-      run(RSTR_K_ROWS, [&] {
-        return launch_act_quant(st, Slices{d->gu, d->s_gu, sg}, B, md.d_ff, md.ffn_geglu, d->act);
+      // few rows: the down projection computes act(gate)*up while staging its
+      // input; shapes it does not serve run the activation launch first
+      bool down_done = false;
+      run(RSTR_K_QGEMM, [&] {
+        const hipError_t r = launch_qgemm_actin(st, W.down, ActIn{d->gu, sg, d->s_gu, md.d_ff, md.ffn_geglu},
+                                                d->mpad, B, d->o, dm, d->s_down, sd);
+        down_done = r == hipSuccess;
+        return r == hipErrorNotSupported ? hipSuccess : r;
       });
-      run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm, d->s_down, sd); });
+      if (!down_done) {
+        run(RSTR_K_ROWS, [&] {
+          return launch_act_quant(st, Slices{d->gu, d->s_gu, sg}, B, md.d_ff, md.ffn_geglu, d->act);
+        });
+        run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.down, d->act, B, d->o, dm, d->s_down, sd); });
+      }
     }
     const float* gnext = (l + 1 < L) ? d->m->layers[l + 1].attn_norm : d->m->final_norm;
     run(RSTR_K_ROWS, [&] {
