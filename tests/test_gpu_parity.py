@@ -587,9 +587,10 @@ def test_lanes_that_read_each_others_appends(sess, name):
 @pytest.mark.parametrize("bits", [4, 8])
 def test_one_lane_long_k_weight_streaming(sess, bits):
     """One lane at Llama-3-8B width (first layer, full vocabulary): the MLP down
-    projection (K = 14336) runs through the weight-streaming GEMV, the other
-    projections through the MFMA tile; tokens and logits equal the oracle's on
-    every step, for Q4 and Q8 weights."""
+    projection (K = 14336) runs through the weight-streaming GEMV, which computes
+    act(gate)*up and its quantisation while staging its input (no separate
+    activation launch); tokens and logits equal the oracle's on every step, for
+    Q4 and Q8 weights."""
     print(f"case one lane llama3_8b q{bits}", flush=True)
     cfg = configs.with_bits(_cfg("llama3_8b", n_layers=1), bits)
     r = _run_lanes(sess, cfg, 1, [300], [[0], [0], [0]], split=256, ps=16, pages=40, pps=30, maxpos=400)
@@ -602,8 +603,9 @@ def test_few_lane_weight_streaming(sess, name, B, bits):
     """Two to four lanes at full config width (first layer, full vocabulary):
     projections with four K slices run on the workgroup GEMV at two rows, and at
     three or four rows for matrices up to 4M weights, and the Qwen3 head (one
-    slice, K = 1024) at two rows (the rest on the MFMA tile); tokens and logits
-    equal the oracle's on every step."""
+    slice, K = 1024) at two rows (the rest on the MFMA tile); a down projection
+    on the workgroup GEMV computes the gated activation in its staging.  Tokens
+    and logits equal the oracle's on every step."""
     print(f"case few lanes {name} B={B} q{bits}", flush=True)
     cfg = configs.with_bits(_cfg(name, n_layers=1), bits)
     prefix = [300, 0, 17, 120][:B]
