@@ -628,6 +628,25 @@ def test_config_shapes_first_layers(sess, name, layers):
     _close(r)
 
 
+@pytest.mark.parametrize("graph", [True, False])
+def test_step_timing_reports_the_last_call(sess, graph):
+    """rstr_decoder_step_timing after rstr_step_lanes calls: every phase is a
+    finite non-negative time, the step's device time is positive, and the host
+    phases of the call fit inside the call's own duration."""
+    print(f"case step timing graph={graph}", flush=True)
+    cfg = configs.TINY_LLAMA
+    r = _run_lanes(sess, cfg, 3, [5, 0, 19], [[0, 1, 2], [0, 2], [0, 1, 2]], graph=graph)
+    try:
+        t = r["d"].step_timing()
+        assert set(t) == set(hip.Decoder.STEP_TIMING)
+        assert all(np.isfinite(v) and v >= 0.0 for v in t.values()), t
+        assert t["device_step"] > 0.0 and t["call"] > 0.0, t
+        host = sum(t[k] for k in ("validate", "prior_sync", "pack", "enqueue", "device_wait", "handback"))
+        assert host <= t["call"] * 1.05 + 1e-3, t
+    finally:
+        _close(r)
+
+
 def test_step_rejects_bad_descriptors(sess):
     cfg = configs.TINY_LLAMA
     m = hip.Model(sess, cfg, seed=1)
