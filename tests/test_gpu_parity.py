@@ -285,6 +285,59 @@ def test_attention_matches_oracle(sess, hd, n_q, n_kv, split, window):
         m.close()
 
 
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (64, 8, 2)])
+@pytest.mark.parametrize("ps,split", [(4, 20), (8, 64), (12, 256), (32, 20), (48, 64), (64, 256), (32, 256),
+                                      (64, 36)])
+@pytest.mark.parametrize("window", [0, 24])
+def test_attention_page_sizes_and_splits_match_oracle(sess, hd, n_q, n_kv, ps, split, window):
+    """Page sizes that are and are not powers of two times 16 (whole-page chunks
+    or per-row page lookups) and splits that are not multiples of the 16-token
+    chunk: the routed attention equals the oracle bit for bit on permuted pages,
+    with empty, one-token, page-boundary and multi-split lanes."""
+    print(f"case attention ps{ps} split{split} window{window} hd{hd}", flush=True)
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
+               head_dim=hd)
+    lengths = np.array([1, 0, ps, ps + 1, 3 * ps - 1, 300, 129], np.int32)
+    B = len(lengths)
+    npg = -(-lengths // ps)
+    pps = int(npg.max())
+    pages = int(npg.sum()) + 3
+    rng = np.random.default_rng(ps * 1000 + split + window + hd)
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        perm = rng.permutation(pages).astype(np.int32)
+        pt = np.full((B, pps), -1, np.int32)
+        used = 0
+        for b in range(B):
+            pt[b, :npg[b]] = perm[used:used + npg[b]]
+            used += npg[b]
+        q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        got = p.attention(0, q, pt, lengths, window=window, scale=scale, split=split)
+        want = O.attention(q, kp, vp, pt, lengths, window, scale, split)
+        assert np.array_equal(got, want)
+    finally:
+        p.close()
+        m.close()
+
+
+@pytest.mark.parametrize("ps,pps,pages", [(8, 40, 200), (32, 10, 60), (12, 26, 130)])
+def test_decode_steps_page_sizes(sess, ps, pps, pages):
+    """Decode steps on pools of 8-, 32- and 12-token pages (whole-page chunks,
+    per-row lookups, routed appends across page boundaries): tokens and logits
+    equal the oracle's on every step."""
+    print(f"case decode ps{ps}", flush=True)
+    cfg = configs.TINY_LLAMA
+    r = _run_lanes(sess, cfg, 4, [5, 0, ps - 1, 2 * ps + 3], [[0, 1, 2, 3], [0, 2, 3], [0, 1, 2, 3], [1, 3]],
+                   split=32, ps=ps, pages=pages, pps=pps, maxpos=pps * ps)
+    _close(r)
+
+
 @pytest.mark.parametrize("hd,n_q,n_kv", [(128, 32, 8), (128, 16, 8), (128, 8, 1), (256, 4, 1), (256, 8, 8),
                                          (128, 8, 8)])
 @pytest.mark.parametrize("split,window", [(256, 0), (64, 40)])
