@@ -7,7 +7,8 @@ copies, primes, one step graph per step) and on the oracle, token for token.
   (seed 1, as the bench runs it), attention split 32 (the bench's split).
 - config3: Qwen3-0.6B-shaped Q4 (28 layers, qk-norm), 64 lanes, contexts
   log-uniform [256, 8192], lanes 0-31 forking one 1024-token prefix with
-  copy-on-write on their first divergent append (attention split 128).
+  copy-on-write on their first divergent append (attention split 256, the
+  bench's split).
 - config5: Llama-3-8B-shaped Q4 (32 layers), 128 lanes with churn (prompts capped
   at 1024 tokens to bound the oracle's host KV memory), and a few lanes at the
   bench's full prompt range (contexts of 3500-4096 tokens through all 32 layers)."""
@@ -65,7 +66,7 @@ def test_config3_shape_schedule_matches_oracle():
     batch, maxpos = 64, 8192 + 64
     pages = 9000
     pl = workload.SharedPrefixPlanner(cfg, batch, 16, pages, maxpos, seed=2)
-    _replay(cfg, pl, batch, pages, maxpos, 128, 2)
+    _replay(cfg, pl, batch, pages, maxpos, 256, 2)
     assert pl.cow_pages > 0
 
 
@@ -100,3 +101,19 @@ def test_config5_shape_full_context_lanes_match_oracle():
     steps = _replay(cfg, pl, batch, pages, maxpos, 256, 2)
     assert all(st["active"] == batch for st in steps)
     assert min(min(st["lengths"]) for st in steps) >= 3500
+
+
+def test_config5_1lane_shape_matches_oracle():
+    """The one-lane end of config5 as the bench runs it: the Llama-3-8B-shaped
+    model with one lane (all 32 layers and the head), attention split 64, a
+    restored prefix drawn from U[3500, 4096]; two planned steps, tokens equal to
+    the oracle's.  At one row every projection streams its weights through a GEMV
+    and the down projection computes the gated activation in its staging."""
+    print("case config5 one lane", flush=True)
+    cfg = configs.LLAMA3_8B
+    batch, maxpos = 1, 4096 + 64
+    pages = maxpos // 16 + 8
+    pl = workload.ChurnPlanner(cfg, batch, 16, pages, maxpos, seed=5, arrival_mean=0.0,
+                               prompt=(3500, 4096), output=(32, 64))
+    steps = _replay(cfg, pl, batch, pages, maxpos, 64, 2)
+    assert all(st["active"] == batch for st in steps)
