@@ -49,7 +49,7 @@ WORKLOADS = {
 
 # workloads whose route pages are a seeded random permutation of the physical pool
 # ("Page tables are a random permutation of the physical page
-# pool"; SURVEY seed 1): the pool's own ids map through workload.PermutedPages
+# pool", permutation seed 1): the pool's own ids map through workload.PermutedPages
 PAGE_PERM_SEEDS = {"config2": 1}
 
 # isolated attention workloads: (model shape, lanes, seed)

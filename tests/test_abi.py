@@ -49,8 +49,8 @@ def header_signatures():
 
 
 def test_ffm_binding_table_matches_the_header():
-    """The FFM downcall table in INTEGRATION.md covers every export with the
-    header's argument and return layouts."""
+    """The Panama FFM downcall table of the integration notes covers every
+    export with the header's argument and return layouts."""
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     block = doc[doc.index("(def ^:private signatures"):]
     block = block[:block.index("})")]
