@@ -566,6 +566,7 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
             dev_ms.append(dec.step_timing()["device_step"])
         probe[label] = round(float(np.median(dev_ms)), 4)
     probe["pause_ms"] = round(1e3 * pause, 3)
+    piped = live_loop_pipelined(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, seed, dec, pool)
     return {"steps": n, "ms_per_step_median": round(1e3 * float(np.median(times)), 3),
             "ms_per_step_mean": round(1e3 * total / n, 3),
             "tokens_per_s_median": round(lanes / float(np.median(times)), 1) if lanes else None,
@@ -575,7 +576,36 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
             # inside rstr_step_lanes (rstr_decoder_step_timing), mean ms per call
             "rstr_step_lanes_phases_ms": phases,
             # the same step's device time (ms, median of 8) back to back and after a host pause
-            "idle_probe_device_step_ms": probe}
+            "idle_probe_device_step_ms": probe,
+            "pipelined": piped}
+
+
+def live_loop_pipelined(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, seed, dec, pool) -> dict:
+    """The same serving loop with the host control plane one step ahead
+    (workload.PipelinedLive): step n+1 is planned while rstr_step_lanes runs step
+    n, so the device receives the sequential loop's calls in the same order and
+    the per-step time is the longer of the two instead of their sum.  Timed as
+    the interval between consecutive step launches."""
+    planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed + 1000, arrival_mean=arrivals,
+                                    prompt=prompt, output=output, page_perm_seed=PAGE_PERM_SEEDS.get(args.workload))
+    loop = workload.PipelinedLive(planner, dec, pool)
+    loop.start()
+    for _ in range(2):  # admissions of the steady-state start, first graph replays
+        loop.step()
+    loop.plan_seconds = 0.0
+    times = []
+    t_prev = time.perf_counter()
+    for _ in range(args.live_steps):
+        loop.step()
+        t = time.perf_counter()
+        times.append(t - t_prev)
+        t_prev = t
+    loop.finish()
+    n = len(times)
+    return {"steps": n, "ms_per_step_median": round(1e3 * float(np.median(times)), 3),
+            "ms_per_step_mean": round(1e3 * sum(times) / n, 3),
+            "tokens_per_s_median": round(lanes / float(np.median(times)), 1) if lanes else None,
+            "host_planning_ms": round(1e3 * loop.plan_seconds / n, 3)}
 
 
 def main():

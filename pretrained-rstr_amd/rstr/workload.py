@@ -265,6 +265,90 @@ class ChurnPlanner:
         return out
 
 
+STEP_DESCRIPTORS = ("slots", "row_offsets", "positions", "page_table", "lengths", "start_positions")
+
+
+class PipelinedLive:
+    """The live serving loop with the host control plane one step ahead of the
+    GPU.  ``planner`` records its steps (a planner built without ``device``);
+    while step n runs inside ``rstr_step_lanes`` on a worker thread (the ctypes
+    call releases the GIL), the planner makes step n+1.  When step n returns,
+    step n+1's fills, copy-on-write copies and primes run on the pool and the
+    decoder in the order the device-resident schedule applies them
+    (``enqueue_staged_prelude``: fills, copies, primes), then step n+1 starts.
+    The device therefore receives the same calls in the same order as in the
+    sequential loop (``LiveDevice``), and only the host's planning overlaps
+    device work.  Planning step n+1 ahead is sound here because the planner's
+    decisions depend on lengths and arrivals, not on token values: pages it
+    frees while step n still reads them are refilled or copied only after step
+    n has returned.
+
+    The worker holds the GIL only around the C call (argument conversion before,
+    the status check after), but the planner thread keeps it for up to the
+    interpreter's switch interval (5 ms by default) once the worker asks for it,
+    which delays the step's launch and its return by as much; the loop runs with
+    a 0.1 ms switch interval and restores the previous one in ``finish``."""
+
+    SWITCH_INTERVAL_S = 1e-4
+
+    def __init__(self, planner, decoder, pool):
+        import concurrent.futures
+        self.planner, self.decoder, self.pool = planner, decoder, pool
+        self.worker = concurrent.futures.ThreadPoolExecutor(max_workers=1)
+        self.fut = None
+        self.plan_seconds = 0.0
+        self._switch = None
+
+    def _apply(self, st):
+        if len(st["fill_pages"]):
+            self.pool.fill_synthetic(st["fill_pages"], st["fill_seed"])
+        for src, dst in st["cow_pairs"]:
+            self.pool.copy_page(int(src), int(dst))
+        if len(st["prime_lanes"]):
+            self.decoder.prime_lanes(st["prime_lanes"], st["prime_tokens"])
+
+    def _plan(self):
+        t0 = time.perf_counter()
+        st = self.planner.plan_step()
+        self.plan_seconds += time.perf_counter() - t0
+        return st
+
+    def _submit(self, st):
+        desc = {k: st[k] for k in STEP_DESCRIPTORS}
+        self.fut = self.worker.submit(self.decoder.step_lanes, **desc)
+
+    def start(self):
+        """Plan and launch the first step."""
+        import sys
+        self._switch = sys.getswitchinterval()
+        sys.setswitchinterval(self.SWITCH_INTERVAL_S)
+        st = self._plan()
+        self._apply(st)
+        self._submit(st)
+        return st
+
+    def step(self):
+        """Plan the next step while the running one finishes; returns the
+        finished step's tokens ([batch] int32) and the step just launched."""
+        st = self._plan()
+        tokens = self.fut.result()
+        self._apply(st)
+        self._submit(st)
+        return tokens, st
+
+    def finish(self):
+        """Wait for the running step; returns its tokens."""
+        import sys
+        try:
+            tokens = self.fut.result()
+        finally:
+            self.fut = None
+            self.worker.shutdown()
+            if self._switch is not None:
+                sys.setswitchinterval(self._switch)
+        return tokens
+
+
 class SharedPrefixPlanner:
     """A fixed set of decode lanes whose first ``shared_lanes`` fork one resident
     prefix: contexts log-uniform in ``ctx``; a lane of

@@ -72,3 +72,52 @@ def test_schedule_replay_with_shared_prefix_forks_matches_oracle():
                                             shared_lanes=3, prefix=64)
     pl = _check(make, batch, pages, maxpos, 32, 12)
     assert pl.cow_pages > 0
+
+
+@pytest.mark.gpu
+def test_pipelined_live_loop_matches_sequential_loop_and_oracle():
+    """The live loop with the control plane one step ahead (PipelinedLive: step
+    n+1 planned while rstr_step_lanes runs step n, its fills and primes applied
+    after step n returns) gives the tokens of the sequential live loop
+    (LiveDevice: every call made as the planner makes it) on the same decoder,
+    step for step, through admissions, retirements and value-based evictions; and
+    the oracle replaying the pipelined loop's recorded steps agrees."""
+    print("case pipelined live loop", flush=True)
+    batch, pages, maxpos, split, n = 6, 60, 192, 16, 30
+    pps = -(-maxpos // 16)
+
+    def make(device=None):
+        return workload.ChurnPlanner(CFG, batch, 16, pages, maxpos, seed=11, arrival_mean=1.5,
+                                     prompt=(8, 60), output=(2, 12), retain_finished=True, device=device)
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=3)
+        p = hip.Pool(m, 16, pages)
+        d = hip.Decoder(m, p, batch, pps, maxpos, split)
+        dev = workload.LiveDevice(d, p)
+        seq_pl = make(dev)
+        seq = []
+        for _ in range(n):
+            seq_pl.plan_step()
+            seq.append(np.array(dev.download_tokens()))
+        pl = make()
+        loop = workload.PipelinedLive(pl, d, p)
+        steps = [loop.start()]
+        piped = []
+        for _ in range(n - 1):
+            tok, st = loop.step()
+            piped.append(np.array(tok))
+            steps.append(st)
+        piped.append(np.array(loop.finish()))
+    assert pl.retired > 0 and pl.evicted > 0
+    om = O.Model(CFG, seed=3)
+    od = O.Decoder(om, batch, 16, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        want = _replay_oracle(od, steps)
+    finally:
+        od.close()
+        om.close()
+    for i, st in enumerate(steps):
+        act = np.asarray(st["lengths"]) > 0
+        assert act.any()
+        assert np.array_equal(piped[i][act], seq[i][act]), (i, piped[i], seq[i])
+        assert np.array_equal(piped[i][act], want[i][act]), (i, piped[i], want[i])
