@@ -81,3 +81,84 @@ def test_permuted_pages_map_every_page_reference_consistently():
             assert sb[lane] // 16 == pt_b.reshape(6, -1)[lane, (n - 1) // 16]
         moved += int((pt_b[pt_b >= 0] != pt_a[pt_a >= 0]).sum())
     assert moved > 0
+
+
+class _FakeDevice:
+    """Stands in for the HIP decoder and pool: records every call with the
+    step it precedes, and checks that no call overlaps a running step."""
+
+    def __init__(self, batch):
+        import threading
+        self.batch, self.log, self.in_step, self.lock = batch, [], False, threading.Lock()
+
+    def _note(self, *ev):
+        with self.lock:
+            assert not self.in_step, ev
+            self.log.append(ev)
+
+    def fill_synthetic(self, pages, seed):
+        self._note("fill", tuple(int(p) for p in pages), int(seed))
+
+    def copy_page(self, src, dst):
+        self._note("copy", int(src), int(dst))
+
+    def prime_lanes(self, lanes, tokens):
+        self._note("prime", tuple(int(x) for x in lanes), tuple(int(x) for x in tokens))
+
+    def step_lanes(self, **desc):
+        import time
+        import numpy as np
+        self._note("step", tuple((k, tuple(np.asarray(v).ravel().tolist())) for k, v in sorted(desc.items())))
+        self.in_step = True
+        time.sleep(0.002)
+        self.in_step = False
+        return np.arange(self.batch, dtype=np.int32)
+
+    def step_timing(self):
+        return {}
+
+
+def _effects(log):
+    """Per step: the filled pages, copies and primed (lane, token) pairs that
+    precede it, then its descriptors."""
+    steps, cur = [], {"fill": set(), "copy": [], "prime": set()}
+    for ev in log:
+        if ev[0] == "fill":
+            cur["fill"] |= {(p, ev[2]) for p in ev[1]}
+        elif ev[0] == "copy":
+            cur["copy"].append(ev[1:])
+        elif ev[0] == "prime":
+            cur["prime"] |= set(zip(ev[1], ev[2]))
+        else:
+            steps.append((cur, ev[1]))
+            cur = {"fill": set(), "copy": [], "prime": set()}
+    return steps
+
+
+def test_pipelined_live_loop_makes_the_sequential_loops_device_calls():
+    """workload.PipelinedLive plans step n+1 while step n runs on its worker
+    thread, then applies step n+1's fills, copies and primes: per step the
+    device receives the same effects and descriptors as from the sequential
+    loop (LiveDevice), none of them while a step is running, through
+    admissions, retirements and value-based evictions."""
+    from rstr.workload import LiveDevice, PipelinedLive
+    kw = dict(batch=6, page_size=16, physical_pages=60, maxpos=192, seed=11, arrival_mean=1.5,
+              prompt=(8, 60), output=(2, 12), retain_finished=True)
+    n = 40
+    seq_dev = _FakeDevice(6)
+    seq = ChurnPlanner(CFG, device=LiveDevice(seq_dev, seq_dev), **kw)
+    for _ in range(n):
+        seq.plan_step()
+    pip_dev = _FakeDevice(6)
+    pl = ChurnPlanner(CFG, **kw)
+    loop = PipelinedLive(pl, pip_dev, pip_dev)
+    loop.start()
+    for _ in range(n - 1):
+        loop.step()
+    loop.finish()
+    assert pl.retired > 0 and pl.evicted > 0
+    a, b = _effects(seq_dev.log), _effects(pip_dev.log)
+    assert len(a) == len(b) == n
+    for i, ((ea, da), (eb, db)) in enumerate(zip(a, b)):
+        assert da == db, i
+        assert ea == eb, i
