@@ -145,10 +145,21 @@ int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported 
 size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                             int32_t* lane_tab, int max_items);
+// The attention output written by the few-item split kernel itself, quantised
+// for the output projection as k_attn_merge writes it (q*d in MFMA tile order,
+// block scales [nb][mpad]).  Only for launches whose every lane's visible
+// range is one split (a merge of one partial) and that run the few-item
+// kernel (attn_direct_out); rows of lanes without items are left as they are.
+struct AttnOut {
+  _Float16* q;
+  float* s;
+  int mpad;
+};
+bool attn_direct_out(const AttnGeom& g, int max_items);
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
                              const int32_t* page_table, int32_t* lane_tab, float* part,
-                             int max_items);
+                             int max_items, const AttnOut* out = nullptr);
 // The decode step's per-row qkv post-processing (launch_qkv_post) done by the
 // few-item attention kernel instead of a launch of its own: each item computes
 // its heads' q from the projection slices (qk-norm, RoPE at the row's position),
@@ -166,7 +177,8 @@ struct AttnQkv {
 };
 bool attn_fuses_qkv(const AttnGeom& g, int max_items);
 hipError_t launch_attn_split_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk,
-                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items);
+                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items,
+                                 const AttnOut* out = nullptr);
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                              int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q);

@@ -2396,7 +2396,7 @@ __global__ __launch_bounds__(256, QKV && G <= 4 ? 3 : 1) void k_attn_split_wg(
     int n_kv, int page_size, int ps_shift, int pps, float scale,
     const float* __restrict__ q, const uint16_t* kp, const uint16_t* vp,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ n_items,
-    const int4* __restrict__ items, float* __restrict__ part, AttnQkv qk) {
+    const int4* __restrict__ items, float* __restrict__ part, AttnQkv qk, AttnOut ao) {
   constexpr int NP = HD / 8;       // 16-byte pieces per row
   constexpr int CT = 16;           // tokens per chunk
   constexpr int CU16 = CT * NP;    // 16-byte units per chunk
@@ -2593,6 +2593,50 @@ __global__ __launch_bounds__(256, QKV && G <= 4 ? 3 : 1) void k_attn_split_wg(
       if (lane == 0) red[wave * G + h] = l[h];
     }
     __syncthreads();
+    if (ao.q) {
+      // The lane's whole visible range is this one split: k_attn_merge's sums
+      // for one partial (w = exp(m - M) with M = m, L = fmaf(l, w, 0),
+      // O = fmaf(o, w, 0) / L) and its quantisation for the output projection,
+      // eight dims per thread, the four threads of a 32-dim block adjacent.
+      const int nb = n_kv * G * HD / 32;
+      for (int e = tid; e < G * HD / 8; e += 256) {
+        const int h = e / (HD / 8), d8 = (e % (HD / 8)) * 8;
+        float m = mx[0];
+#pragma unroll
+        for (int k = 1; k < G; k++)
+          if (h == k) m = mx[k];
+        const float* lc = red;
+        const float w = dexp(m - m);
+        const float L = __builtin_fmaf((lc[h] + lc[G + h]) + (lc[2 * G + h] + lc[3 * G + h]), w, 0.0f);
+        float O[8];
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int c = h * HD + d8 + i;
+          const float o = (comb[0 * G * HD + c] + comb[1 * G * HD + c]) + (comb[2 * G * HD + c] + comb[3 * G * HD + c]);
+          O[i] = __builtin_fmaf(o, w, 0.0f) / L;
+          a = fmaxf(a, fabsf(O[i]));
+        }
+        a = fmaxf(a, xor_lane<1>(a));
+        a = fmaxf(a, xor_lane<2>(a));
+        const float dq = act_scale(a);
+        const float id = (dq != 0.0f) ? 1.0f / dq : 0.0f;
+        const int b = it.b;
+        const int kcol0 = (it.kvh * G + h) * HD + d8;
+        const int blk = kcol0 >> 5, g8 = (kcol0 & 31) >> 3;
+        h8 qv;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          float v = __builtin_rintf(O[i] * id);
+          v = fminf(127.0f, fmaxf(-127.0f, v));
+          qv[i] = (_Float16)(v * dq);
+        }
+        *reinterpret_cast<h8*>(ao.q + ((((size_t)(b >> 4) * nb + blk) * 4 + g8) * 16 + (b & 15)) * 8) = qv;
+        if (g8 == 0) ao.s[(size_t)blk * ao.mpad + b] = dq;
+      }
+      __syncthreads();  // the combine buffer is read before the next item's DMA refills the ring
+      continue;
+    }
     float* rec = part + (size_t)it.idx * G * PF;
     for (int e = tid; e < G * HD / 4; e += 256) {
       const int h = e / (HD / 4), d4 = (e % (HD / 4)) * 4;
@@ -2680,7 +2724,7 @@ struct AttnSplit {
   }
   static void launch(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
                      const uint16_t* vp, const int32_t* pt, int32_t* tab, float* part,
-                     int max_items) {
+                     int max_items, const AttnOut* out) {
     const int R = grid(g, max_items);
     const int32_t* n_items = tab + 4 * g.batch;  // base[batch]
     int* ctr = tab + attn_ctl_offset(g.batch);
@@ -2689,7 +2733,8 @@ struct AttnSplit {
     if constexpr (kWG) {
       if (use_wg(g, max_items)) {
         hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv, g.page_size,
-                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{});
+                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{},
+                           out ? *out : AttnOut{});
         return;
       }
     }
@@ -2698,7 +2743,7 @@ struct AttnSplit {
   }
   // the few-item kernel with the qkv post-processing in its prologue
   static bool launch_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk, const int32_t* pt, int32_t* tab,
-                         float* part, int max_items) {
+                         float* part, int max_items, const AttnOut* out) {
     if constexpr (kWG) {
       if (!use_wg<true>(g, max_items)) return false;
       const int R = std::max(1, std::min(wg_capacity<true>(g), max_items));
@@ -2707,7 +2752,7 @@ struct AttnSplit {
       const int shift = __builtin_ctz((unsigned)g.page_size);
       hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
                          g.page_size, shift, g.pps, g.scale, nullptr, qk.kpages, qk.vpages, pt, n_items, items,
-                         part, qk);
+                         part, qk, out ? *out : AttnOut{});
       return true;
     } else {
       return false;
@@ -2749,15 +2794,23 @@ size_t attn_tab_words(const AttnGeom& g, int max_items) {
 hipError_t launch_attn_split(hipStream_t st, const AttnGeom& g, const float* q,
                              const uint16_t* kpages, const uint16_t* vpages,
                              const int32_t* page_table, int32_t* lane_tab, float* part,
-                             int max_items) {
-#define RSTR_AL(HD_, G_, L_)                                                                            \
-  {                                                                                                     \
-    AttnSplit<HD_, G_, L_>::launch(st, g, q, kpages, vpages, page_table, lane_tab, part, max_items); \
-    return hipGetLastError();                                                                           \
+                             int max_items, const AttnOut* out) {
+  if (out && !attn_direct_out(g, max_items)) return hipErrorInvalidValue;
+#define RSTR_AL(HD_, G_, L_)                                                                                 \
+  {                                                                                                          \
+    AttnSplit<HD_, G_, L_>::launch(st, g, q, kpages, vpages, page_table, lane_tab, part, max_items, out); \
+    return hipGetLastError();                                                                                \
   }
   RSTR_ATTN_DISPATCH(g, RSTR_AL);
 #undef RSTR_AL
   return hipErrorInvalidValue;
+}
+
+bool attn_direct_out(const AttnGeom& g, int max_items) {
+#define RSTR_AD(HD_, G_, L_) return AttnSplit<HD_, G_, L_>::use_wg(g, max_items)
+  RSTR_ATTN_DISPATCH(g, RSTR_AD);
+#undef RSTR_AD
+  return false;
 }
 
 bool attn_fuses_qkv(const AttnGeom& g, int max_items) {
@@ -2769,11 +2822,12 @@ bool attn_fuses_qkv(const AttnGeom& g, int max_items) {
 }
 
 hipError_t launch_attn_split_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk,
-                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items) {
+                                 const int32_t* page_table, int32_t* lane_tab, float* part, int max_items,
+                                 const AttnOut* out) {
   if (g.hd > 256 || g.hd % 4) return hipErrorInvalidValue;
 #define RSTR_AQ(HD_, G_, L_)                                                                                 \
   {                                                                                                         \
-    if (!AttnSplit<HD_, G_, L_>::launch_qkv(st, g, qk, page_table, lane_tab, part, max_items))               \
+    if (!AttnSplit<HD_, G_, L_>::launch_qkv(st, g, qk, page_table, lane_tab, part, max_items, out))          \
       return hipErrorInvalidValue;                                                                          \
     return hipGetLastError();                                                                               \
   }

@@ -163,6 +163,10 @@ struct rstr_decoder {
   // attention kernel, for steps where no lane's visible range holds another
   // lane's appended slot (`mark`: scratch of that check, one word per page)
   bool fuse_qkv = false;
+  // every lane's visible range is one attention split (maxpos <= split) and the
+  // few-item kernel runs: it writes the quantised attention output itself and
+  // the step has no merge launch
+  bool attn_direct = false;
   std::vector<int32_t> mark;
   int32_t* desc = nullptr;                          // device descriptors
   int32_t* lane_tab = nullptr;                      // [2][tabw] attention work tables
@@ -999,6 +1003,9 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   if (d->tabw == 0 && e == hipSuccess) e = hipErrorInvalidValue;
   d->fuse_qkv = head_tail && d->tabw && attn_fuses_qkv(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps,
                                                                 split, 0, md.attn_scale}, d->max_items);
+  d->attn_direct = head_tail && d->tabw && maxpos <= split &&
+                   attn_direct_out(AttnGeom{batch, md.n_q, md.n_kv, md.head_dim, p->page_size, pps, split, 0,
+                                            md.attn_scale}, d->max_items);
   A(dmalloc(&d->lane_tab, 2 * d->tabw));
   A(dmalloc(&d->tokbuf, (size_t)batch));
   A(dmalloc(&d->amax_cand, (size_t)2 * batch * argmax_segments(batch, md.vocab)));
@@ -1284,6 +1291,7 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool
     uint16_t* vp = d->p->slabs[L + l];
     const size_t sq = (size_t)B * d->nqkv, sd = (size_t)B * dm, sg = (size_t)B * 2 * md.d_ff;
     run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.qkv, d->act, B, d->yqkv, d->nqkv, d->s_qkv, sq); });
+    const AttnOut aout{d->act.q, d->act.s, d->act.mpad};
     const float* cos_l = d->rope_cos + (size_t)ti * d->maxpos * half;
     const float* sin_l = d->rope_sin + (size_t)ti * d->maxpos * half;
     if (fused) {
@@ -1291,7 +1299,8 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool
       run(RSTR_K_ATTN_SPLIT, [&] {
         const AttnQkv qk{Slices{d->yqkv, d->s_qkv, sq}, W.q_norm, W.k_norm, goff, md.eps, cos_l, sin_l, pos, slots,
                          len, kp, vp};
-        return launch_attn_split_qkv(st, geo[wi], qk, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
+        return launch_attn_split_qkv(st, geo[wi], qk, pt, d->lane_tab + wi * tabw, d->part, d->max_items,
+                                     d->attn_direct ? &aout : nullptr);
       });
     } else {
       run(RSTR_K_QKV_POST, [&] {
@@ -1299,12 +1308,14 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool
                                md.eps, cos_l, sin_l, pos, slots, d->qr, kp, vp);
       });
       run(RSTR_K_ATTN_SPLIT, [&] {
-        return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, d->lane_tab + wi * tabw, d->part, d->max_items);
+        return launch_attn_split(st, geo[wi], d->qr, kp, vp, pt, d->lane_tab + wi * tabw, d->part, d->max_items,
+                                 d->attn_direct ? &aout : nullptr);
       });
     }
-    run(RSTR_K_ATTN_MERGE, [&] {
-      return launch_attn_merge(st, geo[wi], len, d->lane_tab + wi * tabw, d->part, nullptr, &d->act);
-    });
+    if (!d->attn_direct)
+      run(RSTR_K_ATTN_MERGE, [&] {
+        return launch_attn_merge(st, geo[wi], len, d->lane_tab + wi * tabw, d->part, nullptr, &d->act);
+      });
     run(RSTR_K_QGEMM, [&] { return launch_qgemm(st, W.o, d->act, B, d->o, dm, d->s_o, sd); });
     run(RSTR_K_ROWS, [&] {
       return launch_post_attn(st, Slices{d->o, d->s_o, sd}, d->r0, d->xmid, W.post_attn_norm, W.ffn_pre_norm, goff, md.eps, B,

@@ -48,10 +48,9 @@ def _generate(device, pool_device):
     return dec.generate("c", prompt, 64)
 
 
-def test_config1_gemma_q8_one_lane_64_greedy_steps():
-    print("case config1 gemma q8", flush=True)
+def _config1_case(split):
     om = O.Model(CFG, seed=SEED)
-    od = O.Decoder(om, 1, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=SPLIT)
+    od = O.Decoder(om, 1, PS, PAGES, PPS, MAXPOS, kv_f16=True, split=split)
     try:
         want = _generate(OracleStepDevice(od), od)
         want_logits = od.logits()
@@ -61,12 +60,26 @@ def test_config1_gemma_q8_one_lane_64_greedy_steps():
     with hip.Session(0) as sess:
         m = hip.Model(sess, CFG, seed=SEED)
         p = hip.Pool(m, PS, PAGES)
-        d = hip.Decoder(m, p, 1, PPS, MAXPOS, SPLIT)
+        d = hip.Decoder(m, p, 1, PPS, MAXPOS, split)
         got = _generate(HipStepDevice(d), p)
         got_logits = d.logits()
     assert len(got) == 64
     assert got == want
     assert np.array_equal(got_logits.view(np.uint32), want_logits.view(np.uint32))
+
+
+def test_config1_gemma_q8_one_lane_64_greedy_steps():
+    print("case config1 gemma q8", flush=True)
+    _config1_case(SPLIT)
+
+
+def test_config1_single_split_writes_attention_output_directly():
+    """The same run with a split of at least the decoder's maxpos: every visible
+    range is one split, so the few-item attention kernel writes the quantised
+    attention output itself and the step has no merge launch; tokens and final
+    logits equal the oracle's at that split, bit for bit."""
+    print("case config1 single split", flush=True)
+    _config1_case(128)
 
 
 def _teacher_forced(step, prime, routes, seq, greedy_from=None):

@@ -576,17 +576,19 @@ def test_few_item_attention_with_qkv_prologue_group_sizes(sess, n_q, n_kv, hd):
         _close(r)
 
 
-@pytest.mark.parametrize("name", ["tiny_gemma", "tiny_qwen"])
-def test_lanes_that_read_each_others_appends(sess, name):
+@pytest.mark.parametrize("name,split", [("tiny_gemma", 16), ("tiny_qwen", 16), ("tiny_qwen", 128)])
+def test_lanes_that_read_each_others_appends(sess, name, split):
     """Small batches run the qkv post-processing inside the few-item attention
     kernel, where each lane appends its own new K/V row.  A step whose lanes read
     each other's new rows (three causal lanes over one route, as a prefill tile
     lays them out) must still see every append, as the oracle's append-then-attend
     order does: the decoder runs such a step with the separate qkv launch.  Later
-    steps on private routes return to the fused form."""
-    print(f"case shared appends {name}", flush=True)
+    steps on private routes return to the fused form.  At split 128 >= maxpos
+    (head dim 128) both forms also write the attention output from the split
+    kernel, without a merge launch."""
+    print(f"case shared appends {name} split {split}", flush=True)
     cfg = configs.MODELS[name]
-    B, ps, pages, pps, maxpos, split = 3, 16, 12, 6, 96, 16
+    B, ps, pages, pps, maxpos = 3, 16, 12, 6, 96
     start_len = 37
     pt = np.full((B, pps), -1, np.int32)
     route = np.array([7, 2, 9, 4], np.int32)

@@ -121,3 +121,36 @@ def test_pipelined_live_loop_matches_sequential_loop_and_oracle():
         assert act.any()
         assert np.array_equal(piped[i][act], seq[i][act]), (i, piped[i], seq[i])
         assert np.array_equal(piped[i][act], want[i][act]), (i, piped[i], want[i])
+
+
+@pytest.mark.gpu
+def test_schedule_replay_single_split_direct_output_matches_oracle():
+    """Lanes whose visible range is one attention split (maxpos <= split) on a
+    head dimension the few-item kernel serves (the tiny Qwen shape, 128): the
+    split kernel writes the quantised attention output itself and the step has
+    no merge launch.  Continuous churn (lanes retire, idle and refill) replayed
+    against the oracle at the same split, token for token."""
+    print("case schedule single split", flush=True)
+    cfg = configs.MODELS["tiny_qwen"]
+    batch, pages, maxpos, split, n_steps = 6, 60, 192, 256, 40
+    pps = -(-maxpos // 16)
+    pl = workload.ChurnPlanner(cfg, batch, 16, pages, maxpos, seed=11, arrival_mean=1.5,
+                               prompt=(8, 60), output=(2, 12), retain_finished=True)
+    steps = [pl.plan_step() for _ in range(n_steps)]
+    assert pl.retired > 0
+    om = O.Model(cfg, seed=3)
+    od = O.Decoder(om, batch, 16, pages, pps, maxpos, kv_f16=True, split=split)
+    try:
+        want = _replay_oracle(od, steps)
+    finally:
+        od.close()
+        om.close()
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, cfg, seed=3)
+        p = hip.Pool(m, 16, pages)
+        d = hip.Decoder(m, p, batch, pps, maxpos, split)
+        d.schedule_upload(steps)
+        got, _ = d.schedule_run(0, n_steps)
+    for i, st in enumerate(steps):
+        act = np.asarray(st["lengths"]) > 0
+        assert np.array_equal(got[i][act], want[i][act]), (i, got[i], want[i])
