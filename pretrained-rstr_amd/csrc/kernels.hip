@@ -2391,7 +2391,7 @@ __device__ void attn_qkv_prologue(const AttnQkv& qk, const AttnItem& it, int n_k
 // by the item that holds it, so no separate qkv launch precedes this one.
 // (The QKV form keeps three waves per SIMD for G <= 4: a few kernel-constant
 // prologue values then live in scratch and are reloaded once per item.)
-template <int HD, int G, int RB, bool QKV = false>
+template <int HD, int G, int RB, bool QKV = false, bool DIRECT = false>
 __global__ __launch_bounds__(256, QKV && G <= 4 ? 3 : 1) void k_attn_split_wg(
     int n_kv, int page_size, int ps_shift, int pps, float scale,
     const float* __restrict__ q, const uint16_t* kp, const uint16_t* vp,
@@ -2593,7 +2593,7 @@ __global__ __launch_bounds__(256, QKV && G <= 4 ? 3 : 1) void k_attn_split_wg(
       if (lane == 0) red[wave * G + h] = l[h];
     }
     __syncthreads();
-    if (ao.q) {
+    if constexpr (DIRECT) {
       // The lane's whole visible range is this one split: k_attn_merge's sums
       // for one partial (w = exp(m - M) with M = m, L = fmaf(l, w, 0),
       // O = fmaf(o, w, 0) / L) and its quantisation for the output projection,
@@ -2732,9 +2732,13 @@ struct AttnSplit {
     const int shift = pg16(g) ? __builtin_ctz((unsigned)g.page_size) : 0;
     if constexpr (kWG) {
       if (use_wg(g, max_items)) {
-        hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv, g.page_size,
-                           shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{},
-                           out ? *out : AttnOut{});
+        if (out)
+          hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, false, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
+                             g.page_size, shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{},
+                             *out);
+        else
+          hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv, g.page_size,
+                             shift, g.pps, g.scale, q, kp, vp, pt, n_items, items, part, AttnQkv{}, AttnOut{});
         return;
       }
     }
@@ -2750,9 +2754,14 @@ struct AttnSplit {
       const int32_t* n_items = tab + 4 * g.batch;
       const int4* items = reinterpret_cast<const int4*>(tab + attn_items_offset(g.batch));
       const int shift = __builtin_ctz((unsigned)g.page_size);
-      hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
-                         g.page_size, shift, g.pps, g.scale, nullptr, qk.kpages, qk.vpages, pt, n_items, items,
-                         part, qk, out ? *out : AttnOut{});
+      if (out)
+        hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, true, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
+                           g.page_size, shift, g.pps, g.scale, nullptr, qk.kpages, qk.vpages, pt, n_items, items,
+                           part, qk, *out);
+      else
+        hipLaunchKernelGGL((k_attn_split_wg<HD, G, RBW, true>), dim3(R), dim3(256), lds_wg(g), st, g.n_kv,
+                           g.page_size, shift, g.pps, g.scale, nullptr, qk.kpages, qk.vpages, pt, n_items, items,
+                           part, qk, AttnOut{});
       return true;
     } else {
       return false;
