@@ -322,31 +322,53 @@ class PipelinedLive:
         import sys
         self._switch = sys.getswitchinterval()
         sys.setswitchinterval(self.SWITCH_INTERVAL_S)
-        st = self._plan()
-        self._apply(st)
-        self._submit(st)
+        try:
+            st = self._plan()
+            self._apply(st)
+            self._submit(st)
+        except BaseException:
+            self._teardown()
+            raise
         return st
 
     def step(self):
         """Plan the next step while the running one finishes; returns the
-        finished step's tokens ([batch] int32) and the step just launched."""
-        st = self._plan()
-        tokens = self.fut.result()
-        self._apply(st)
-        self._submit(st)
+        finished step's tokens ([batch] int32) and the step just launched.  On
+        an error the running step is waited for, the worker stopped and the
+        switch interval restored before the error propagates."""
+        try:
+            st = self._plan()
+            tokens = self.fut.result()
+            self._apply(st)
+            self._submit(st)
+        except BaseException:
+            self._teardown()
+            raise
         return tokens, st
 
     def finish(self):
         """Wait for the running step; returns its tokens."""
-        import sys
         try:
             tokens = self.fut.result()
-        finally:
             self.fut = None
-            self.worker.shutdown()
-            if self._switch is not None:
-                sys.setswitchinterval(self._switch)
+        finally:
+            self._teardown()
         return tokens
+
+    def _teardown(self):
+        """No step left running on the decoder, the worker stopped, the
+        interpreter's switch interval as before ``start``."""
+        import sys
+        if self.fut is not None:
+            try:
+                self.fut.result()
+            except BaseException:
+                pass
+            self.fut = None
+        self.worker.shutdown()
+        if self._switch is not None:
+            sys.setswitchinterval(self._switch)
+            self._switch = None
 
 
 class SharedPrefixPlanner:

@@ -162,3 +162,34 @@ def test_pipelined_live_loop_makes_the_sequential_loops_device_calls():
     for i, ((ea, da), (eb, db)) in enumerate(zip(a, b)):
         assert da == db, i
         assert ea == eb, i
+
+
+def test_pipelined_live_loop_error_waits_for_the_running_step_and_restores_the_interpreter():
+    """A failing step surfaces from the next PipelinedLive.step after the step
+    still running has finished; the switch interval is restored."""
+    import sys
+    from rstr.workload import PipelinedLive
+
+    class Failing(_FakeDevice):
+        def __init__(self, batch):
+            super().__init__(batch)
+            self.steps = 0
+
+        def step_lanes(self, **desc):
+            self.steps += 1
+            out = super().step_lanes(**desc)
+            if self.steps == 3:
+                raise RuntimeError("device step failed")
+            return out
+    before = sys.getswitchinterval()
+    dev = Failing(6)
+    pl = ChurnPlanner(CFG, batch=6, page_size=16, physical_pages=60, maxpos=192, seed=11, arrival_mean=1.5,
+                      prompt=(8, 60), output=(2, 12))
+    loop = PipelinedLive(pl, dev, dev)
+    loop.start()
+    with pytest.raises(RuntimeError, match="device step failed"):
+        for _ in range(10):
+            loop.step()
+    assert sys.getswitchinterval() == before
+    assert loop.fut is None and not dev.in_step
+    assert dev.steps == 3
