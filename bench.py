@@ -674,17 +674,18 @@ def main():
         for extra, steps in (("config5_1lane", 100), ("config2", 200), ("config3", 40)):
             sub_run(extra, decode_workload, decode_keys, steps=steps, warmup=10,
                     live_steps=min(args.live_steps, 10),
-                    no_cpu_baseline=args.no_cpu_baseline or extra in ("config5_1lane", "config3"),
-                    cpu_seconds=min(args.cpu_seconds, 6.0))
+                    no_cpu_baseline=args.no_cpu_baseline or extra == "config5_1lane",
+                    cpu_seconds=min(args.cpu_seconds, 6.0 if extra == "config2" else 4.0))
         sub_run("config1", config1_workload,
                 ("value", "unit", "ms_per_step", "steps", "config", "roofline", "cpu_baseline"), warmup=1)
         sub_run("config4", attention_workload,
-                ("metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms"),
-                steps=20, warmup=3, no_cpu_baseline=True)
+                ("metric", "value", "unit", "ms_per_step", "config", "roofline", "merge_ms", "cpu_baseline"),
+                steps=20, warmup=3, cpu_seconds=min(args.cpu_seconds, 4.0))
         # the bulk prefill tile beside the step (chunk5 keeps its own line: its host-link
         # rate after the runs above reads ~30 GB/s against ~56 GB/s in a fresh process)
-        sub_run("prefill5", prefill_workload, ("metric", "value", "unit", "ms_per_step", "config", "roofline"),
-                steps=2, warmup=1, no_cpu_baseline=True)
+        sub_run("prefill5", prefill_workload,
+                ("metric", "value", "unit", "ms_per_step", "config", "roofline", "cpu_baseline"),
+                steps=2, warmup=1, cpu_seconds=min(args.cpu_seconds, 4.0))
     print(json.dumps(out), flush=True)
 
 
