@@ -145,6 +145,11 @@ int attn_grid(const AttnGeom& g, int max_items);              // 0: unsupported 
 size_t attn_tab_words(const AttnGeom& g, int max_items);      // 0: unsupported geometry
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                             int32_t* lane_tab, int max_items);
+// The work lists of n_geo (1 or 2) geometries that share batch, split and
+// lengths (lane tables `tab_stride` words apart): one launch for batches of
+// up to 1024 lanes.
+hipError_t launch_attn_lists(hipStream_t st, const AttnGeom* g, int n_geo, const int32_t* lengths,
+                             int32_t* lane_tab, size_t tab_stride, int max_items);
 // The attention output written by the few-item split kernel itself, quantised
 // for the output projection as k_attn_merge writes it (q*d in MFMA tile order,
 // block scales [nb][mpad]).  Only for launches whose every lane's visible

@@ -1787,6 +1787,181 @@ __global__ __launch_bounds__(256) void k_attn_items(int batch, int n_kv, int spl
   items[pos] = int4{b | (kvh << 20), t0, t1, i};
 }
 
+// k_attn_prep and k_attn_items in one workgroup, for batches of up to 1024
+// lanes: the lane tables are written to `tab` as k_attn_prep writes them (the
+// split and merge kernels read them), and the work list is built from LDS
+// copies of the lane prefix, with the partial items' buckets and fill cursors
+// in LDS.  One workgroup per geometry, so the windowed and the global layers'
+// tables of a step take one launch.  The per-lane and per-item rules are
+// those of the two kernels; the list is the same up to the order inside one
+// partial bucket, which no consumer depends on.
+struct AttnListArgs {
+  int window[2], R[2];
+  int32_t* tab[2];
+  int4* items[2];
+};
+__global__ __launch_bounds__(1024) void k_attn_list(int batch, int split, int n_kv, int max_items,
+                                                    const int32_t* __restrict__ lengths, AttnListArgs args) {
+  __shared__ int32_t s_a[1024], s_f[1024], s_p[1024], s_h[RSTR_NCH], s_cur[RSTR_NCH];
+  __shared__ int32_t s_lo[1024], s_k0[1024], s_ns[1024], s_len[1024], s_base[1025], s_fb[1025];
+  const int gsel = blockIdx.x;
+  const int window = args.window[gsel], R = args.R[gsel];
+  int32_t* tab = args.tab[gsel];
+  int4* items = args.items[gsel];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < RSTR_NCH; i += 1024) {
+    s_h[i] = 0;
+    s_cur[i] = 0;
+  }
+  __syncthreads();
+  // ---- lane tables (k_attn_prep, one chunk of lanes)
+  const int b = tid;
+  int l0 = 0, kk0 = 0, n = 0, f = 0, len = 0;
+  if (b < batch) {
+    len = lengths[b];
+    if (len > 0) {
+      l0 = window > 0 ? max(0, len - window) : 0;
+      kk0 = l0 / split;
+      n = (len - 1) / split - kk0 + 1;
+      const int f_t1 = min(len, (kk0 + 1) * split);
+      const bool first_full = l0 == kk0 * split && f_t1 - l0 == split;
+      const bool last_full = len % split == 0;
+      f = n == 1 ? (first_full ? 1 : 0) : n - (first_full ? 0 : 1) - (last_full ? 0 : 1);
+      if (!first_full) atomicAdd(&s_h[(f_t1 - (l0 & ~15) + 15) >> 4], n_kv);
+      if (n > 1 && !last_full) {
+        const int lt0 = (kk0 + n - 1) * split;
+        atomicAdd(&s_h[(len - (lt0 & ~15) + 15) >> 4], n_kv);
+      }
+    }
+  }
+  const int32_t va = b < batch ? n * n_kv : 0;
+  const int32_t vf = b < batch ? f * n_kv : 0;
+  const int32_t vp = va - vf;
+  s_a[tid] = va;
+  s_f[tid] = vf;
+  s_p[tid] = vp;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t ta = tid >= off ? s_a[tid - off] : 0;
+    const int32_t tf = tid >= off ? s_f[tid - off] : 0;
+    const int32_t tp = tid >= off ? s_p[tid - off] : 0;
+    __syncthreads();
+    s_a[tid] += ta;
+    s_f[tid] += tf;
+    s_p[tid] += tp;
+    __syncthreads();
+  }
+  int32_t tot_a = s_a[1023], tot_f = s_f[1023], tot_p = s_p[1023];
+  int32_t base_b = s_a[tid] - va, fb_b = s_f[tid] - vf, pb_b = s_p[tid] - vp;
+  // more items than the list holds (descriptors the host validation rejects):
+  // no attention work, every output 0 (as k_attn_prep)
+  const bool over = tot_a > max_items;
+  if (over) {
+    n = 0;
+    base_b = fb_b = pb_b = 0;
+    tot_a = tot_f = tot_p = 0;
+  }
+  if (b < batch) {
+    tab[b] = l0;
+    tab[batch + b] = kk0;
+    tab[2 * batch + b] = n;
+    tab[3 * batch + b] = base_b;
+    tab[4 * batch + 1 + b] = fb_b;
+    tab[5 * batch + 2 + b] = pb_b;
+  }
+  s_lo[tid] = l0;
+  s_k0[tid] = kk0;
+  s_ns[tid] = n;
+  s_len[tid] = len;
+  s_base[tid] = base_b;
+  s_fb[tid] = fb_b;
+  __syncthreads();  // the scans' arrays are read before they are reused below
+  if (over)
+    for (int i = tid; i < RSTR_NCH; i += 1024) s_h[i] = 0;
+  if (tid == 0) {
+    s_base[batch] = tot_a;
+    s_fb[batch] = tot_f;
+    tab[3 * batch + batch] = tot_a;
+    tab[4 * batch + 1 + batch] = tot_f;
+    tab[5 * batch + 2 + batch] = tot_p;
+    const int arm = attn_static_rounds(tot_a, R) * R;
+    tab[attn_ctl_offset(batch)] = arm;
+    tab[attn_ctl_offset(batch) + 1] = arm;
+  }
+  __syncthreads();
+  // partial items by decreasing chunk count: boff[c] = the partial items of
+  // all counts above c (exclusive suffix sum; thread r holds count NCH-1-r)
+  static_assert(RSTR_NCH <= 1024, "one count per thread");
+  const int32_t hv = tid < RSTR_NCH ? s_h[RSTR_NCH - 1 - tid] : 0;
+  s_a[tid] = hv;
+  __syncthreads();
+  for (int off = 1; off < RSTR_NCH; off <<= 1) {
+    const int32_t t = tid >= off ? s_a[tid - off] : 0;
+    __syncthreads();
+    s_a[tid] += t;
+    __syncthreads();
+  }
+  int32_t* s_boff = s_p;  // the last scan's array is free again
+  if (tid < RSTR_NCH) s_boff[RSTR_NCH - 1 - tid] = s_a[tid] - hv;
+  __syncthreads();
+  // ---- the work list (k_attn_items)
+  for (int i = tid; i < tot_a; i += 1024) {
+    int bl = 0, hi = batch;
+    while (hi - bl > 1) {
+      const int mid = (bl + hi) >> 1;
+      if (s_base[mid] <= i) bl = mid; else hi = mid;
+    }
+    const int ns = s_ns[bl];
+    const int rel = i - s_base[bl];
+    const int kvh = rel / ns;
+    const int sp = rel % ns;
+    const int ln = s_len[bl];
+    const int k = s_k0[bl] + sp;
+    const int t0 = max(s_lo[bl], k * split), t1 = min(ln, (k + 1) * split);
+    const int nf = (s_fb[bl + 1] - s_fb[bl]) / n_kv;
+    const int lb = s_lo[bl];
+    const bool first_partial = !(lb == s_k0[bl] * split && min(ln, (s_k0[bl] + 1) * split) - lb == split);
+    const int before = (first_partial && sp > 0) ? 1 : 0;
+    int pos;
+    if (t1 - t0 == split) {
+      pos = s_fb[bl] + kvh * nf + (sp - before);
+    } else {
+      const int nch = (t1 - (t0 & ~15) + 15) >> 4;
+      pos = tot_f + s_boff[nch] + atomicAdd(&s_cur[nch], 1);
+    }
+    items[pos] = int4{bl | (kvh << 20), t0, t1, i};
+  }
+}
+
+// The step's work lists of up to two geometries (windowed and global layers)
+// sharing lengths, split and max_items: one launch for batches of up to 1024
+// lanes, else k_attn_prep + k_attn_items per geometry.
+hipError_t launch_attn_lists(hipStream_t st, const AttnGeom* g, int n_geo, const int32_t* lengths,
+                             int32_t* lane_tab, size_t tab_stride, int max_items) {
+  if (n_geo < 1 || n_geo > 2) return hipErrorInvalidValue;
+  if (g[0].batch > 1024) {
+    for (int w = 0; w < n_geo; w++) {
+      const hipError_t e = launch_attn_prep(st, g[w], lengths, lane_tab + w * tab_stride, max_items);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  AttnListArgs a{};
+  for (int w = 0; w < n_geo; w++) {
+    if (g[w].batch != g[0].batch || g[w].split != g[0].split || g[w].n_kv != g[0].n_kv) return hipErrorInvalidValue;
+    const int R = attn_grid(g[w], max_items);
+    if (R <= 0) return hipErrorInvalidValue;
+    if (g[w].n_kv >= (1 << 11)) return hipErrorInvalidValue;
+    a.window[w] = g[w].window;
+    a.R[w] = R;
+    a.tab[w] = lane_tab + w * tab_stride;
+    a.items[w] = reinterpret_cast<int4*>(a.tab[w] + attn_items_offset(g[w].batch));
+  }
+  hipLaunchKernelGGL(k_attn_list, dim3(n_geo), dim3(1024), 0, st, g[0].batch, g[0].split, g[0].n_kv, max_items,
+                     lengths, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_attn_prep(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                             int32_t* lane_tab, int max_items) {
   const int R = attn_grid(g, max_items);

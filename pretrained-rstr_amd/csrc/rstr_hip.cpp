@@ -1274,9 +1274,7 @@ static hipError_t enqueue_step(rstr_decoder* d, hipStream_t st, Prof* prof, bool
                       w == 1 ? md.sliding_window : 0, md.attn_scale};
   }
   const size_t tabw = d->tabw;
-  run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[0], len, d->lane_tab, d->max_items); });
-  if (has_window)
-    run(RSTR_K_ROWS, [&] { return launch_attn_prep(st, geo[1], len, d->lane_tab + tabw, d->max_items); });
+  run(RSTR_K_ROWS, [&] { return launch_attn_lists(st, geo, has_window ? 2 : 1, len, d->lane_tab, tabw, d->max_items); });
   run(RSTR_K_ROWS, [&] {
     return launch_rms_quant(st, d->r0, d->m->layers[0].attn_norm, goff, md.eps, B, dm, d->act);
   });
@@ -1872,7 +1870,7 @@ extern "C" int rstr_attention_run(rstr_pool* p, int32_t layer, int32_t batch, in
   geo.scale = scale;
   hipStream_t st = s->stream;
   int L = p->m->d.n_layers;
-  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab, max_items));
+  HIPCHK(s, launch_attn_lists(st, &geo, 1, bf.len, bf.tab, 0, max_items));
   HIPCHK(s, launch_attn_split(st, geo, bf.q, p->slabs[layer], p->slabs[L + layer], bf.pt, bf.tab, bf.part,
                               max_items));
   HIPCHK(s, launch_attn_merge(st, geo, bf.len, bf.tab, bf.part, bf.out, nullptr));
@@ -1936,7 +1934,7 @@ extern "C" int rstr_attention_run_static(rstr_pool* p, int32_t layer, int32_t ba
   HIPCHK(s, hipMemcpy(dq, q, qb, hipMemcpyHostToDevice));
   HIPCHK(s, hipMemcpy(dpt, page_table, ptb, hipMemcpyHostToDevice));
   HIPCHK(s, hipMemcpy(dlen, lengths, lb, hipMemcpyHostToDevice));
-  HIPCHK(s, launch_attn_prep(st, geo, dlen, dtab, max_items));
+  HIPCHK(s, launch_attn_lists(st, &geo, 1, dlen, dtab, 0, max_items));
   HIPCHK(s, launch_attn_split(st, geo, dq, p->slabs[layer], p->slabs[L + layer], dpt, dtab, dpart, max_items));
   HIPCHK(s, launch_attn_merge(st, geo, dlen, dtab, dpart, dout, nullptr));
   HIPCHK(s, hipStreamSynchronize(st));
@@ -1959,7 +1957,7 @@ extern "C" int rstr_attention_bench(rstr_pool* p, int32_t layer, int32_t batch, 
   geo.scale = scale;
   hipStream_t st = s->stream;
   int L = p->m->d.n_layers;
-  HIPCHK(s, launch_attn_prep(st, geo, bf.len, bf.tab, max_items));
+  HIPCHK(s, launch_attn_lists(st, &geo, 1, bf.len, bf.tab, 0, max_items));
   std::vector<hipEvent_t> ev(4 * iters);
   for (auto& e : ev) HIPCHK(s, hipEventCreate(&e));
   for (int i = 0; i < iters; i++) {
