@@ -3127,24 +3127,115 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
   }
 }
 
+// The same merge with one wave per (lane, q head, 64 dims), one dim per lane,
+// for grids too small to fill the GPU: a wave holds one value per split and
+// loads C splits at once (64 for head dim 256, 32 below), one dependent memory
+// round trip per C splits instead of per 16.  Every dim's sums are the same
+// fmaf chains in split order as above, and L, M and w are formed identically
+// by the head's waves.
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_merge_wide(int batch, int n_q, int n_kv,
+                                                   const int32_t* __restrict__ lengths,
+                                                   int32_t* __restrict__ tab,
+                                                   const float* __restrict__ part,
+                                                   float* __restrict__ out_f32,
+                                                   _Float16* __restrict__ Q, float* __restrict__ S,
+                                                   int mpad) {
+  constexpr int NQB = HD / 64;         // 64-dim blocks of a head, one wave each
+  constexpr int C = HD >= 256 ? 64 : 32;  // splits loaded at once
+  const int lane = threadIdx.x;
+  const int bh = blockIdx.x / NQB, qb = blockIdx.x % NQB;
+  const int b = bh / n_q, h = bh % n_q;
+  const int G = n_q / n_kv;
+  // the split kernel of this layer has finished: re-arm its claim counter
+  // for the next split over this table
+  if (blockIdx.x == 0 && lane == 0) tab[attn_ctl_offset(batch)] = tab[attn_ctl_offset(batch) + 1];
+  const int ns = tab[2 * batch + b];
+  const int base = tab[3 * batch + b] + (h / G) * ns;
+  const int hl = h % G;
+  const int len = lengths[b];
+  const int dim = qb * 64 + lane;
+  float O = 0.0f;
+  if (len > 0 && ns > 0) {
+    const int stride = G * attn_part_floats(HD);
+    const float* pb = part + (size_t)base * stride + hl * attn_part_floats(HD);
+    float ov[C];
+#pragma unroll
+    for (int j = 0; j < C; j++) ov[j] = pb[(size_t)min(j, ns - 1) * stride + dim];
+    const float* p0 = pb + (size_t)min(lane, ns - 1) * stride;
+    const float m0 = p0[HD], l0 = p0[HD + 1];
+    float M = m0;
+    for (int kk = lane + 64; kk < ns; kk += 64) M = fmaxf(M, pb[(size_t)kk * stride + HD]);
+    M = wave_max(M);
+    float L = 0.0f, wl = 0.0f, ll = 0.0f;
+    for (int c0 = 0; c0 < ns; c0 += C) {
+      // w_k = exp(m_k - M) by lane k mod 64, read from that lane
+      if (c0 == 0) {
+        wl = dexp(m0 - M);
+        ll = l0;
+      } else if (c0 % 64 == 0) {
+        const float* pk = pb + (size_t)min(c0 + lane, ns - 1) * stride;
+        wl = dexp(pk[HD] - M);
+        ll = pk[HD + 1];
+      }
+      if (c0 > 0) {
+#pragma unroll
+        for (int j = 0; j < C; j++) ov[j] = pb[(size_t)min(c0 + j, ns - 1) * stride + dim];
+      }
+      const int gn = min(C, ns - c0), l0off = c0 % 64;
+#pragma unroll
+      for (int j = 0; j < C; j++) {
+        if (j < gn) {
+          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), l0off + j));
+          const float lk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ll), l0off + j));
+          L = __builtin_fmaf(lk, w, L);
+          O = __builtin_fmaf(ov[j], w, O);
+        }
+      }
+    }
+    O = O / L;
+  }
+  if (out_f32) out_f32[((size_t)b * n_q + h) * HD + dim] = O;
+  if (Q) {
+    // 32-dim blocks: 32 lanes per block
+    float a = fabsf(O);
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
+    const float dq = act_scale(a);
+    const float id = (dq != 0.0f) ? 1.0f / dq : 0.0f;
+    const int qd = n_q * HD, nb = qd >> 5;
+    const int kcol = h * HD + dim;
+    float v = __builtin_rintf(O * id);
+    v = fminf(127.0f, fmaxf(-127.0f, v));
+    const int blk = kcol >> 5, g = (kcol & 31) >> 3, s = kcol & 7;
+    Q[((((size_t)(b >> 4) * nb + blk) * 4 + g) * 16 + (b & 15)) * 8 + s] = (_Float16)(v * dq);
+    if ((kcol & 31) == 0) S[(size_t)blk * mpad + b] = dq;
+  }
+}
+
 hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* lengths,
                              int32_t* lane_tab, const float* part, float* out_f32,
                              ActBuf* out_q) {
-  dim3 grid(g.batch * g.n_q);
   _Float16* Q = out_q ? out_q->q : nullptr;
   float* S = out_q ? out_q->s : nullptr;
   int mpad = out_q ? out_q->mpad : 0;
+  // under one (lane, head) wave per SIMD the merge is latency bound: spread
+  // each head over HD/64 waves; above, one wave per head does less work per
+  // output
+  const bool wide = g.batch * g.n_q < 1024;
+  dim3 grid(g.batch * g.n_q * (wide ? g.hd / 64 : 1));
+#define RSTR_MERGE(HDV)                                                                                  \
+  hipLaunchKernelGGL(wide ? k_attn_merge_wide<HDV> : k_attn_merge<HDV>, grid, dim3(64), 0, st, g.batch, \
+                     g.n_q, g.n_kv, lengths, lane_tab, part, out_f32, Q, S, mpad)
   if (g.hd == 64)
-    hipLaunchKernelGGL(k_attn_merge<64>, grid, dim3(64), 0, st, g.batch, g.n_q, g.n_kv, lengths,
-                       lane_tab, part, out_f32, Q, S, mpad);
+    RSTR_MERGE(64);
   else if (g.hd == 128)
-    hipLaunchKernelGGL(k_attn_merge<128>, grid, dim3(64), 0, st, g.batch, g.n_q, g.n_kv, lengths,
-                       lane_tab, part, out_f32, Q, S, mpad);
+    RSTR_MERGE(128);
   else if (g.hd == 256)
-    hipLaunchKernelGGL(k_attn_merge<256>, grid, dim3(64), 0, st, g.batch, g.n_q, g.n_kv, lengths,
-                       lane_tab, part, out_f32, Q, S, mpad);
+    RSTR_MERGE(256);
   else
     return hipErrorInvalidValue;
+#undef RSTR_MERGE
   return hipGetLastError();
 }
 

@@ -206,12 +206,26 @@ def test_attention_many_splits_matches_oracle(sess, hd, n_q, n_kv, split, window
     """Routes of up to 69 splits: the merge's rounds of 16 splits and its second
     group of 64 (exp weights read from the lane that computed them)."""
     print(f"case attention many splits hd{hd} q{n_q} kv{n_kv} split{split} window{window}", flush=True)
+    _many_splits_case(sess, hd, n_q, n_kv, split, window, 6)
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv,B", [(128, 32, 8, 31), (128, 32, 8, 32), (256, 8, 2, 127),
+                                           (256, 8, 2, 128)])
+def test_attention_merge_forms_match_oracle(sess, hd, n_q, n_kv, B):
+    """Both merge forms on routes of up to 69 splits: one wave per (lane, head)
+    from 1024 (lane, head) pairs on, one wave per 64 dims of a head below (32
+    or 64 splits per load round, the second group of 64 splits)."""
+    print(f"case attention merge forms hd{hd} q{n_q} kv{n_kv} B{B}", flush=True)
+    _many_splits_case(sess, hd, n_q, n_kv, 16, 0, B)
+
+
+def _many_splits_case(sess, hd, n_q, n_kv, split, window, B):
     cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
                head_dim=hd)
-    lengths = np.array([1100, 300, 0, 1025, 17, 257], np.int32)
-    B, ps, pps = len(lengths), 16, 72
+    lengths = np.resize(np.array([1100, 300, 0, 1025, 17, 257], np.int32), B)
+    ps, pps = 16, 72
     pages = int(sum(-(-n // ps) for n in lengths)) + 4
-    rng = np.random.default_rng(hd * 7 + split + window)
+    rng = np.random.default_rng(hd * 7 + split + window + B)
     m = hip.Model(sess, cfg, seed=2)
     p = hip.Pool(m, ps, pages)
     try:
