@@ -219,6 +219,37 @@ def test_attention_merge_forms_match_oracle(sess, hd, n_q, n_kv, B):
     _many_splits_case(sess, hd, n_q, n_kv, 16, 0, B)
 
 
+@pytest.mark.parametrize("lo,hi", [(1024, 1800), (2100, 2600)])
+def test_attention_long_lists_match_oracle(sess, lo, hi):
+    """Long lists on the one-wave split kernel (128 lanes, 32/8 heads, hd 128,
+    split 256): 4-10 full splits per lane are 2-5 rounds of full items on
+    MI355X's 2048 resident waves, so static rounds and the claim phase both
+    run.  Pages are drawn with repetition from a small pool (lanes share
+    pages).  Bit-exact against the oracle."""
+    print(f"case attention long lists ctx [{lo}, {hi})", flush=True)
+    hd, n_q, n_kv, B, ps, split = 128, 32, 8, 128, 16, 256
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv, head_dim=hd)
+    rng = np.random.default_rng(lo)
+    lengths = rng.integers(lo, hi, B).astype(np.int32)
+    pages, pps = 384, int(-(-lengths.max() // ps))
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        pt = rng.integers(0, pages, (B, pps)).astype(np.int32)
+        q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        got = p.attention(0, q, pt, lengths, window=0, scale=scale, split=split)
+        want = O.attention(q, kp, vp, pt, lengths, 0, scale, split)
+        assert np.array_equal(got, want)
+    finally:
+        p.close()
+        m.close()
+
+
 def _many_splits_case(sess, hd, n_q, n_kv, split, window, B):
     cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
                head_dim=hd)
