@@ -250,6 +250,38 @@ def test_attention_long_lists_match_oracle(sess, lo, hi):
         m.close()
 
 
+@pytest.mark.parametrize("window", [0, 40])
+def test_attention_over_1024_lanes_matches_oracle(sess, window):
+    """1100 lanes: past the one-workgroup list kernel's 1024 lanes, so the work
+    list comes from the lane-table kernel (a scan carried across two 1024-lane
+    chunks) and the item writer; contexts 0..160 at split 32 (empty lanes,
+    partial first and last splits, windows).  Bit-exact against the oracle."""
+    print(f"case attention 1100 lanes window {window}", flush=True)
+    hd, n_q, n_kv, B, ps, split = 64, 4, 2, 1100, 16, 32
+    cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv, head_dim=hd)
+    rng = np.random.default_rng(1100 + window)
+    lengths = rng.integers(0, 161, B).astype(np.int32)
+    lengths[::97] = 0
+    pages, pps = 256, int(-(-lengths.max() // ps))
+    m = hip.Model(sess, cfg, seed=2)
+    p = hip.Pool(m, ps, pages)
+    try:
+        kp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        vp = rng.standard_normal((pages, ps, n_kv, hd)).astype(np.float16)
+        p.upload(0, 0, 0, kp)
+        p.upload(1, 0, 0, vp)
+        pt = rng.integers(0, pages, (B, pps)).astype(np.int32)
+        q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+        scale = 1.0 / math.sqrt(hd)
+        got = p.attention(0, q, pt, lengths, window=window, scale=scale, split=split)
+        want = O.attention(q, kp, vp, pt, lengths, window, scale, split)
+        assert np.array_equal(got, want)
+        assert np.all(got[lengths == 0] == 0)
+    finally:
+        p.close()
+        m.close()
+
+
 def _many_splits_case(sess, hd, n_q, n_kv, split, window, B):
     cfg = _cfg("tiny_llama", n_layers=1, d_model=128, d_ff=128, vocab=64, n_q=n_q, n_kv=n_kv,
                head_dim=hd)
