@@ -2850,16 +2850,29 @@ static int device_cus() {
 // wave per workgroup, every wave resident, never more waves than items).
 template <int HD, int G, int LPT>
 struct AttnSplit {
+  // Ring depth of the one-wave kernel: RB, or RB - 1 where the shallower
+  // ring lets more waves reside on a CU (instantiations whose LDS, not their
+  // registers, bound the occupancy: config3's Qwen3 geometry at split 256
+  // goes from 10 to 12 waves per CU, 3.85-3.89 -> 3.75-3.79 ms/step; the
+  // Llama geometry is register-bound at 8 waves either way and keeps RB).
   static constexpr int RB = RSTR_ATTN_RING;
-  static size_t lds(const AttnGeom& g) {
-    return (size_t)RB * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
+  static constexpr int RBS = RSTR_ATTN_RING - 1;
+  static size_t lds(const AttnGeom& g, int rb) {
+    return (size_t)rb * 16 * (HD / 8) * 16 + (size_t)((G * HD * 4 + 1023) / 1024) * 1024 +
            sizeof(float) * G * g.split;
   }
   // whole-page chunks: page_size a power of two and a multiple of 16
   static bool pg16(const AttnGeom& g) { return g.page_size % 16 == 0 && (g.page_size & (g.page_size - 1)) == 0; }
-  static decltype(&k_attn_split<HD, G, LPT, true, RB>) kernel(const AttnGeom& g) {
+  static decltype(&k_attn_split<HD, G, LPT, true, RB>) kernel(const AttnGeom& g, int rb) {
+    if (rb == RBS) return pg16(g) ? k_attn_split<HD, G, LPT, true, RBS> : k_attn_split<HD, G, LPT, false, RBS>;
     return pg16(g) ? k_attn_split<HD, G, LPT, true, RB> : k_attn_split<HD, G, LPT, false, RB>;
   }
+  static int waves_per_cu(const AttnGeom& g, int rb) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel(g, rb), 64, lds(g, rb)) != hipSuccess) return 0;
+    return n;
+  }
+  static int ring(const AttnGeom& g) { return waves_per_cu(g, RBS) > waves_per_cu(g, RB) ? RBS : RB; }
   // Few-item launches (k_attn_split_wg, one 4-wave workgroup per item): head
   // dim 128 or 256, whole-page chunks, and a largest work list that fits in
   // two rounds of resident workgroups.  Its ring is 32 KB deep.
@@ -2893,8 +2906,8 @@ struct AttnSplit {
   }
   static int grid(const AttnGeom& g, int max_items) {
     if (use_wg(g, max_items)) return std::max(1, std::min(wg_capacity(g), max_items));
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel(g), 64, lds(g)) != hipSuccess || n <= 0) n = 2;
+    int n = waves_per_cu(g, ring(g));
+    if (n <= 0) n = 2;
     return std::max(1, std::min(device_cus() * n, max_items));
   }
   static void launch(hipStream_t st, const AttnGeom& g, const float* q, const uint16_t* kp,
@@ -2917,8 +2930,9 @@ struct AttnSplit {
         return;
       }
     }
-    hipLaunchKernelGGL(kernel(g), dim3(R), dim3(64), lds(g), st, g.n_kv, g.page_size, shift, g.pps, g.scale, q,
-                       kp, vp, pt, n_items, items, ctr, part);
+    const int rb = ring(g);
+    hipLaunchKernelGGL(kernel(g, rb), dim3(R), dim3(64), lds(g, rb), st, g.n_kv, g.page_size, shift, g.pps, g.scale,
+                       q, kp, vp, pt, n_items, items, ctr, part);
   }
   // the few-item kernel with the qkv post-processing in its prologue
   static bool launch_qkv(hipStream_t st, const AttnGeom& g, const AttnQkv& qk, const int32_t* pt, int32_t* tab,
