@@ -3233,10 +3233,10 @@ hipError_t launch_attn_merge(hipStream_t st, const AttnGeom& g, const int32_t* l
   _Float16* Q = out_q ? out_q->q : nullptr;
   float* S = out_q ? out_q->s : nullptr;
   int mpad = out_q ? out_q->mpad : 0;
-  // under one (lane, head) wave per SIMD the merge is latency bound: spread
+  // under two (lane, head) waves per SIMD the merge is latency bound: spread
   // each head over HD/64 waves; above, one wave per head does less work per
   // output
-  const bool wide = g.batch * g.n_q < 1024;
+  const bool wide = g.batch * g.n_q < 2048;
   dim3 grid(g.batch * g.n_q * (wide ? g.hd / 64 : 1));
 #define RSTR_MERGE(HDV)                                                                                  \
   hipLaunchKernelGGL(wide ? k_attn_merge_wide<HDV> : k_attn_merge<HDV>, grid, dim3(64), 0, st, g.batch, \

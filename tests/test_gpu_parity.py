@@ -209,11 +209,11 @@ def test_attention_many_splits_matches_oracle(sess, hd, n_q, n_kv, split, window
     _many_splits_case(sess, hd, n_q, n_kv, split, window, 6)
 
 
-@pytest.mark.parametrize("hd,n_q,n_kv,B", [(128, 32, 8, 31), (128, 32, 8, 32), (256, 8, 2, 127),
-                                           (256, 8, 2, 128)])
+@pytest.mark.parametrize("hd,n_q,n_kv,B", [(128, 32, 8, 63), (128, 32, 8, 64), (256, 8, 2, 255),
+                                           (256, 8, 2, 256)])
 def test_attention_merge_forms_match_oracle(sess, hd, n_q, n_kv, B):
     """Both merge forms on routes of up to 69 splits: one wave per (lane, head)
-    from 1024 (lane, head) pairs on, one wave per 64 dims of a head below (32
+    from 2048 (lane, head) pairs on, one wave per 64 dims of a head below (32
     or 64 splits per load round, the second group of 64 splits)."""
     print(f"case attention merge forms hd{hd} q{n_q} kv{n_kv} B{B}", flush=True)
     _many_splits_case(sess, hd, n_q, n_kv, 16, 0, B)
