@@ -30,8 +30,8 @@ METRIC = "aggregate decode tokens/sec at N lanes; % of HBM roofline (GB/s) on 1 
 HBM_PEAK_GBS = 8000.0
 
 # attention split per workload (the split fixes the canonical reduction order, so it is a
-# decoder parameter): the fastest of 16..512 measured on MI355X for each workload
-SPLITS = {"config5": 256, "config5_1lane": 64, "config3": 256, "config2": 32, "config4": 256, "prefill5": 256,
+# decoder parameter): the fastest of 16..1024 measured on MI355X for each workload
+SPLITS = {"config5": 256, "config5_1lane": 64, "config3": 640, "config2": 32, "config4": 256, "prefill5": 256,
           "config1": 128,
           "chunk5": 256}
 

@@ -7,7 +7,7 @@ copies, primes, one step graph per step) and on the oracle, token for token.
   (seed 1, as the bench runs it), attention split 32 (the bench's split).
 - config3: Qwen3-0.6B-shaped Q4 (28 layers, qk-norm), 64 lanes, contexts
   log-uniform [256, 8192], lanes 0-31 forking one 1024-token prefix with
-  copy-on-write on their first divergent append (attention split 256, the
+  copy-on-write on their first divergent append (attention split 640, the
   bench's split).
 - config5: Llama-3-8B-shaped Q4 (32 layers), 128 lanes with churn (prompts capped
   at 1024 tokens to bound the oracle's host KV memory), and a few lanes at the
@@ -66,7 +66,7 @@ def test_config3_shape_schedule_matches_oracle():
     batch, maxpos = 64, 8192 + 64
     pages = 9000
     pl = workload.SharedPrefixPlanner(cfg, batch, 16, pages, maxpos, seed=2)
-    _replay(cfg, pl, batch, pages, maxpos, 256, 2)
+    _replay(cfg, pl, batch, pages, maxpos, 640, 2)
     assert pl.cow_pages > 0
 
 
