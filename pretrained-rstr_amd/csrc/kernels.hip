@@ -3142,7 +3142,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(int batch, int n_q, int n_kv,
 }
 
 // The same merge with one wave per (lane, q head, 64 dims), one dim per lane,
-// for grids too small to fill the GPU: a wave holds one value per split and
+// for grids of under two (lane, head) waves per SIMD, where the merge is
+// latency bound: a wave holds one value per split and
 // loads C splits at once (64 for head dim 256, 32 below), one dependent memory
 // round trip per C splits instead of per 16.  Every dim's sums are the same
 // fmaf chains in split order as above, and L, M and w are formed identically
