@@ -582,10 +582,11 @@ def live_loop(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, 
 
 def live_loop_pipelined(args, cfg, lanes, ps, physical, maxpos, prompt, output, arrivals, seed, dec, pool) -> dict:
     """The same serving loop with the host control plane one step ahead
-    (workload.PipelinedLive): step n+1 is planned while rstr_step_lanes runs step
-    n, so the device receives the sequential loop's calls in the same order and
-    the per-step time is the longer of the two instead of their sum.  Timed as
-    the interval between consecutive step launches."""
+    (workload.PipelinedLive): step n is submitted (rstr_step_lanes_submit), step
+    n+1 is planned while the device runs it, applied and submitted before step
+    n's tokens are collected, so the device receives the sequential loop's calls
+    in the same order and the per-step time is the longer of the two instead of
+    their sum.  Timed as the interval between consecutive collected steps."""
     planner = workload.ChurnPlanner(cfg, lanes, ps, physical, maxpos, seed=seed + 1000, arrival_mean=arrivals,
                                     prompt=prompt, output=output, page_perm_seed=PAGE_PERM_SEEDS.get(args.workload))
     loop = workload.PipelinedLive(planner, dec, pool)

@@ -205,6 +205,20 @@ int rstr_prime_rows(rstr_decoder* d, int32_t n, const int32_t* lanes, const floa
 int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int32_t* row_offsets,
                     const int32_t* positions, const int32_t* page_table, const int32_t* lengths,
                     const int32_t* start_positions, int32_t* tokens_out);
+/* No counterpart in the reference (step-lanes! is synchronous): the same step
+ * without waiting for it, for callers that plan the next step while the
+ * device runs this one.  Validates and copies the descriptors (same meaning
+ * and errors as rstr_step_lanes), enqueues the step and returns.  At most two
+ * submitted steps are in flight (a third submit fails with RSTR_E_STATE);
+ * rstr_step_lanes_collect waits for the oldest one and writes its tokens.
+ * Every other call on the decoder, pool or session runs after the submitted
+ * steps in stream order. */
+int rstr_step_lanes_submit(rstr_decoder* d, const int32_t* slots, const int32_t* row_offsets,
+                           const int32_t* positions, const int32_t* page_table, const int32_t* lengths,
+                           const int32_t* start_positions);
+/* No counterpart in the reference: the tokens of the oldest submitted step
+ * (RSTR_E_STATE when none is in flight). */
+int rstr_step_lanes_collect(rstr_decoder* d, int32_t* tokens_out);
 /* No counterpart in the reference: a measurement helper for the serving
  * loop's timing harness (continuation/benchmark.clj:180-194 times whole
  * step-lanes! calls).  The phases of the decoder's last rstr_step_lanes call,

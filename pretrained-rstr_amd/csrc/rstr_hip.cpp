@@ -193,6 +193,12 @@ struct rstr_decoder {
   // phases of the last rstr_step_lanes call (rstr_decoder_step_timing)
   hipEvent_t ev_step[2] = {nullptr, nullptr};
   double step_ms[RSTR_STEP_TIMING_FIELDS] = {};
+  // steps submitted without waiting (rstr_step_lanes_submit / _collect): two
+  // pinned descriptor and token slots, the in-flight steps in submission order
+  int32_t* h_desc_q[2] = {nullptr, nullptr};
+  int32_t* h_tok_q[2] = {nullptr, nullptr};
+  hipEvent_t ev_q[2] = {nullptr, nullptr};
+  int q_first = 0, q_n = 0;
 };
 
 // ---------------------------------------------------------------------------
@@ -931,6 +937,11 @@ static void decoder_free(rstr_decoder* d) {
   if (d->h_tok) hipHostFree(d->h_tok);
   for (hipEvent_t ev : d->ev_step)
     if (ev) hipEventDestroy(ev);
+  for (int i = 0; i < 2; i++) {
+    if (d->h_desc_q[i]) hipHostFree(d->h_desc_q[i]);
+    if (d->h_tok_q[i]) hipHostFree(d->h_tok_q[i]);
+    if (d->ev_q[i]) hipEventDestroy(d->ev_q[i]);
+  }
   delete d;
 }
 
@@ -1015,6 +1026,11 @@ static int decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pps,
   if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_tok, sizeof(int32_t) * batch);
   for (hipEvent_t& ev : d->ev_step)
     if (e == hipSuccess) e = hipEventCreate(&ev);
+  for (int i = 0; i < 2; i++) {
+    if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_desc_q[i], sizeof(int32_t) * d->desc_words);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&d->h_tok_q[i], sizeof(int32_t) * batch);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&d->ev_q[i], hipEventDisableTiming);
+  }
   if (e != hipSuccess) {
     decoder_free(d);
     return fail(s, RSTR_E_OOM, std::string("decoder allocation: ") + hipGetErrorString(e));
@@ -1418,6 +1434,50 @@ extern "C" int rstr_step_lanes(rstr_decoder* d, const int32_t* slots, const int3
   const double v[RSTR_STEP_TIMING_FIELDS] = {ms(t0, t1), ms(t1, t2), ms(t2, t3), ms(t3, t4), ms(t4, t5), ms(t5, t6),
                                              ms(t0, t6), (double)dev};
   std::memcpy(d->step_ms, v, sizeof v);
+  return RSTR_OK;
+}
+
+
+// The same step without waiting for it (no counterpart in the reference,
+// whose step-lanes! is synchronous): validation, descriptor packing into one
+// of two pinned slots, the descriptor copy, the step graph and the token copy
+// are enqueued on the session's stream and the call returns.  At most two
+// steps are in flight; rstr_step_lanes_collect returns their tokens in
+// submission order.  Calls that synchronise the stream (priming, page copies,
+// fills, rstr_step_lanes) run after the submitted steps, in stream order.
+extern "C" int rstr_step_lanes_submit(rstr_decoder* d, const int32_t* slots, const int32_t* row_offsets,
+                                      const int32_t* positions, const int32_t* page_table,
+                                      const int32_t* lengths, const int32_t* start_positions) {
+  if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
+  rstr_session* s = d->m->s;
+  if (!d->head_tail) return fail(s, RSTR_E_STATE, "a bulk-prefill decoder has no head; use rstr_prefill_range");
+  if (d->q_n >= 2) return fail(s, RSTR_E_STATE, "two submitted steps are in flight: collect one first");
+  bool fused = false;
+  int rc = validate_step(d, slots, row_offsets, positions, page_table, lengths, start_positions, &fused);
+  if (rc) return rc;
+  HIPCHK(s, hipSetDevice(s->device));
+  // this slot's previous step was collected, so its staging is free
+  const int slot = (d->q_first + d->q_n) % 2;
+  pack_desc(d, d->h_desc_q[slot], slots, row_offsets, positions, page_table, lengths, start_positions);
+  HIPCHK(s, hipMemcpyAsync(d->desc, d->h_desc_q[slot], sizeof(int32_t) * d->desc_words, hipMemcpyHostToDevice,
+                           s->stream));
+  if ((rc = run_step_device(d, fused))) return rc;
+  HIPCHK(s, hipMemcpyAsync(d->h_tok_q[slot], d->tokbuf, sizeof(int32_t) * d->B, hipMemcpyDeviceToHost, s->stream));
+  HIPCHK(s, hipEventRecord(d->ev_q[slot], s->stream));
+  d->q_n++;
+  return RSTR_OK;
+}
+
+extern "C" int rstr_step_lanes_collect(rstr_decoder* d, int32_t* tokens_out) {
+  if (!d) return fail(nullptr, RSTR_E_INVALID, "null decoder");
+  rstr_session* s = d->m->s;
+  if (d->q_n == 0) return fail(s, RSTR_E_STATE, "no submitted step is in flight");
+  if (!tokens_out) return fail(s, RSTR_E_INVALID, "null token output");
+  const int slot = d->q_first;
+  HIPCHK(s, hipEventSynchronize(d->ev_q[slot]));
+  std::memcpy(tokens_out, d->h_tok_q[slot], sizeof(int32_t) * d->B);
+  d->q_first = (slot + 1) % 2;
+  d->q_n--;
   return RSTR_OK;
 }
 

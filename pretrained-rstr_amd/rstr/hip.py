@@ -28,6 +28,7 @@ EXPORTS = (
     "rstr_pool_upload", "rstr_pool_download", "rstr_pool_fill_synthetic", "rstr_chunk_export_submit",
     "rstr_chunk_restore_submit", "rstr_transfer_done", "rstr_transfer_complete", "rstr_chunk_bench", "rstr_decoder_open",
     "rstr_decoder_close", "rstr_prime_lanes", "rstr_prime_rows", "rstr_step_lanes",
+    "rstr_step_lanes_submit", "rstr_step_lanes_collect",
     "rstr_decode_logits", "rstr_decoder_read_rows", "rstr_decoder_set_graph", "rstr_decoder_step_timing",
     "rstr_prefill_open",
     "rstr_prefill_range", "rstr_append_run", "rstr_tail_run", "rstr_linear_run",
@@ -117,6 +118,8 @@ def lib():
             "rstr_prime_lanes": (i32, [P, i32, P, P]),
             "rstr_prime_rows": (i32, [P, i32, P, P]),
             "rstr_step_lanes": (i32, [P, P, P, P, P, P, P, P]),
+            "rstr_step_lanes_submit": (i32, [P, P, P, P, P, P, P]),
+            "rstr_step_lanes_collect": (i32, [P, P]),
             "rstr_decode_logits": (i32, [P, P]),
             "rstr_decoder_read_rows": (i32, [P, P]),
             "rstr_decoder_set_graph": (i32, [P, i32]),
@@ -485,6 +488,17 @@ class Decoder:
         args = [_i32(a) for a in (slots, row_offsets, positions, page_table, lengths, start_positions)]
         out = np.empty(self.batch, np.int32)
         self.sess.check(lib().rstr_step_lanes(self.h, *[_p(a) for a in args], _p(out)))
+        return out
+
+    def step_lanes_submit(self, slots, row_offsets, positions, page_table, lengths, start_positions):
+        """Enqueue one step without waiting (rstr_step_lanes_submit); at most two in flight."""
+        args = [_i32(a) for a in (slots, row_offsets, positions, page_table, lengths, start_positions)]
+        self.sess.check(lib().rstr_step_lanes_submit(self.h, *[_p(a) for a in args]))
+
+    def step_lanes_collect(self) -> np.ndarray:
+        """Tokens of the oldest submitted step (rstr_step_lanes_collect)."""
+        out = np.empty(self.batch, np.int32)
+        self.sess.check(lib().rstr_step_lanes_collect(self.h, _p(out)))
         return out
 
     def logits(self) -> np.ndarray:

@@ -270,34 +270,23 @@ STEP_DESCRIPTORS = ("slots", "row_offsets", "positions", "page_table", "lengths"
 
 class PipelinedLive:
     """The live serving loop with the host control plane one step ahead of the
-    GPU.  ``planner`` records its steps (a planner built without ``device``);
-    while step n runs inside ``rstr_step_lanes`` on a worker thread (the ctypes
-    call releases the GIL), the planner makes step n+1.  When step n returns,
-    step n+1's fills, copy-on-write copies and primes run on the pool and the
-    decoder in the order the device-resident schedule applies them
-    (``enqueue_staged_prelude``: fills, copies, primes), then step n+1 starts.
-    The device therefore receives the same calls in the same order as in the
-    sequential loop (``LiveDevice``), and only the host's planning overlaps
-    device work.  Planning step n+1 ahead is sound here because the planner's
-    decisions depend on lengths and arrivals, not on token values: pages it
-    frees while step n still reads them are refilled or copied only after step
-    n has returned.
-
-    The worker holds the GIL only around the C call (argument conversion before,
-    the status check after), but the planner thread keeps it for up to the
-    interpreter's switch interval (5 ms by default) once the worker asks for it,
-    which delays the step's launch and its return by as much; the loop runs with
-    a 0.1 ms switch interval and restores the previous one in ``finish``."""
-
-    SWITCH_INTERVAL_S = 1e-4
+    GPU, in one thread.  ``planner`` records its steps (a planner built without
+    ``device``).  Step n is enqueued with ``rstr_step_lanes_submit`` and the
+    planner makes step n+1 while the device runs it; step n+1's fills,
+    copy-on-write copies and primes then run on the pool and the decoder in the
+    order the device-resident schedule applies them (``enqueue_staged_prelude``:
+    fills, copies, primes) -- each of those calls runs after step n in stream
+    order -- step n+1 is submitted, and only then are step n's tokens
+    collected.  The device receives the same calls in the same order as in the
+    sequential loop (``LiveDevice``).  Planning step n+1 ahead is sound here
+    because the planner's decisions depend on lengths and arrivals, not on
+    token values: pages it frees while step n still reads them are refilled or
+    copied only after step n, in stream order."""
 
     def __init__(self, planner, decoder, pool):
-        import concurrent.futures
         self.planner, self.decoder, self.pool = planner, decoder, pool
-        self.worker = concurrent.futures.ThreadPoolExecutor(max_workers=1)
-        self.fut = None
+        self.inflight = 0
         self.plan_seconds = 0.0
-        self._switch = None
 
     def _apply(self, st):
         if len(st["fill_pages"]):
@@ -314,14 +303,15 @@ class PipelinedLive:
         return st
 
     def _submit(self, st):
-        desc = {k: st[k] for k in STEP_DESCRIPTORS}
-        self.fut = self.worker.submit(self.decoder.step_lanes, **desc)
+        self.decoder.step_lanes_submit(**{k: st[k] for k in STEP_DESCRIPTORS})
+        self.inflight += 1
+
+    def _collect(self):
+        self.inflight -= 1
+        return self.decoder.step_lanes_collect()
 
     def start(self):
-        """Plan and launch the first step."""
-        import sys
-        self._switch = sys.getswitchinterval()
-        sys.setswitchinterval(self.SWITCH_INTERVAL_S)
+        """Plan and submit the first step."""
         try:
             st = self._plan()
             self._apply(st)
@@ -332,15 +322,15 @@ class PipelinedLive:
         return st
 
     def step(self):
-        """Plan the next step while the running one finishes; returns the
-        finished step's tokens ([batch] int32) and the step just launched.  On
-        an error the running step is waited for, the worker stopped and the
-        switch interval restored before the error propagates."""
+        """Plan and submit the next step while the running one finishes;
+        returns the finished step's tokens ([batch] int32) and the step just
+        submitted.  On an error every submitted step is collected before the
+        error propagates."""
         try:
             st = self._plan()
-            tokens = self.fut.result()
             self._apply(st)
             self._submit(st)
+            tokens = self._collect()
         except BaseException:
             self._teardown()
             raise
@@ -349,26 +339,18 @@ class PipelinedLive:
     def finish(self):
         """Wait for the running step; returns its tokens."""
         try:
-            tokens = self.fut.result()
-            self.fut = None
+            tokens = self._collect()
         finally:
             self._teardown()
         return tokens
 
     def _teardown(self):
-        """No step left running on the decoder, the worker stopped, the
-        interpreter's switch interval as before ``start``."""
-        import sys
-        if self.fut is not None:
+        """No submitted step left in flight on the decoder."""
+        while self.inflight > 0:
             try:
-                self.fut.result()
+                self._collect()
             except BaseException:
-                pass
-            self.fut = None
-        self.worker.shutdown()
-        if self._switch is not None:
-            sys.setswitchinterval(self._switch)
-            self._switch = None
+                self.inflight = 0
 
 
 class SharedPrefixPlanner:

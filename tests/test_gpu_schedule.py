@@ -77,11 +77,12 @@ def test_schedule_replay_with_shared_prefix_forks_matches_oracle():
 @pytest.mark.gpu
 def test_pipelined_live_loop_matches_sequential_loop_and_oracle():
     """The live loop with the control plane one step ahead (PipelinedLive: step
-    n+1 planned while rstr_step_lanes runs step n, its fills and primes applied
-    after step n returns) gives the tokens of the sequential live loop
-    (LiveDevice: every call made as the planner makes it) on the same decoder,
-    step for step, through admissions, retirements and value-based evictions; and
-    the oracle replaying the pipelined loop's recorded steps agrees."""
+    n submitted with rstr_step_lanes_submit, step n+1 planned while it runs,
+    its fills and primes applied and step n+1 submitted before step n's tokens
+    are collected) gives the tokens of the sequential live loop (LiveDevice:
+    every call made as the planner makes it) on the same decoder, step for
+    step, through admissions, retirements and value-based evictions; and the
+    oracle replaying the pipelined loop's recorded steps agrees."""
     print("case pipelined live loop", flush=True)
     batch, pages, maxpos, split, n = 6, 60, 192, 16, 30
     pps = -(-maxpos // 16)
@@ -154,3 +155,63 @@ def test_schedule_replay_single_split_direct_output_matches_oracle():
     for i, st in enumerate(steps):
         act = np.asarray(st["lengths"]) > 0
         assert np.array_equal(got[i][act], want[i][act]), (i, got[i], want[i])
+
+
+def _lane_desc(lengths, pps, ps=16):
+    """Descriptors of lanes whose routes hold pages b*pps .. b*pps+pps-1, every
+    active lane appending its last token."""
+    B = len(lengths)
+    pt = np.full((B, pps), -1, np.int32)
+    slots = np.full(B, -1, np.int32)
+    pos = np.zeros(B, np.int32)
+    for b, L in enumerate(lengths):
+        if L:
+            pt[b, :-(-L // ps)] = b * pps + np.arange(-(-L // ps))
+            slots[b] = pt[b, (L - 1) // ps] * ps + (L - 1) % ps
+            pos[b] = L - 1
+    return dict(slots=slots, row_offsets=np.arange(B + 1, dtype=np.int32), positions=pos,
+                page_table=pt.ravel(), lengths=np.asarray(lengths, np.int32),
+                start_positions=np.zeros(B, np.int32))
+
+
+@pytest.mark.gpu
+def test_submitted_steps_equal_synchronous_steps():
+    """rstr_step_lanes_submit / _collect: two steps in flight, a prime and a
+    page copy issued between submissions (they run after the submitted steps in
+    stream order), then the tokens collected in submission order, equal the
+    synchronous rstr_step_lanes sequence on a twin decoder, tokens and resident
+    rows; a third submission and a collection with nothing in flight fail with
+    a state error and leave the decoder usable."""
+    print("case submitted steps", flush=True)
+    batch, pps, maxpos, split = 3, 4, 64, 16
+    steps = [[5, 9, 0], [6, 10, 0], [7, 11, 3]]
+    with hip.Session(0) as sess:
+        m = hip.Model(sess, CFG, seed=3)
+        twins = []
+        for _ in range(2):
+            p = hip.Pool(m, 16, batch * pps)
+            p.fill_synthetic(np.arange(batch * pps, dtype=np.int32), 5)
+            twins.append((p, hip.Decoder(m, p, batch, pps, maxpos, split)))
+        (p1, d1), (p2, d2) = twins
+        for p, d in twins:
+            d.prime_lanes([0, 1], [3, 17])
+        sync = []
+        for i, L in enumerate(steps):
+            if i == 2:
+                d1.prime_lanes([2], [29])
+                p1.copy_page(1, 2 * pps)
+            sync.append(d1.step_lanes(**_lane_desc(L, pps)))
+        d2.step_lanes_submit(**_lane_desc(steps[0], pps))
+        d2.step_lanes_submit(**_lane_desc(steps[1], pps))
+        with pytest.raises(hip.RstrError, match="in flight"):
+            d2.step_lanes_submit(**_lane_desc(steps[2], pps))
+        got = [d2.step_lanes_collect()]
+        d2.prime_lanes([2], [29])
+        p2.copy_page(1, 2 * pps)
+        d2.step_lanes_submit(**_lane_desc(steps[2], pps))
+        got += [d2.step_lanes_collect(), d2.step_lanes_collect()]
+        with pytest.raises(hip.RstrError, match="no submitted step"):
+            d2.step_lanes_collect()
+        for i in range(3):
+            assert np.array_equal(got[i], sync[i]), (i, got[i], sync[i])
+        assert np.array_equal(d2.rows(), d1.rows())

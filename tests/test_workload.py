@@ -84,17 +84,16 @@ def test_permuted_pages_map_every_page_reference_consistently():
 
 
 class _FakeDevice:
-    """Stands in for the HIP decoder and pool: records every call with the
-    step it precedes, and checks that no call overlaps a running step."""
+    """Stands in for the HIP decoder and pool: records every call in stream
+    order with the step it precedes (a call made while submitted steps are in
+    flight runs after them, as on the session's stream), and checks that at
+    most two submitted steps are in flight."""
 
     def __init__(self, batch):
-        import threading
-        self.batch, self.log, self.in_step, self.lock = batch, [], False, threading.Lock()
+        self.batch, self.log, self.inflight = batch, [], 0
 
     def _note(self, *ev):
-        with self.lock:
-            assert not self.in_step, ev
-            self.log.append(ev)
+        self.log.append(ev)
 
     def fill_synthetic(self, pages, seed):
         self._note("fill", tuple(int(p) for p in pages), int(seed))
@@ -106,12 +105,21 @@ class _FakeDevice:
         self._note("prime", tuple(int(x) for x in lanes), tuple(int(x) for x in tokens))
 
     def step_lanes(self, **desc):
-        import time
         import numpy as np
+        assert self.inflight == 0
         self._note("step", tuple((k, tuple(np.asarray(v).ravel().tolist())) for k, v in sorted(desc.items())))
-        self.in_step = True
-        time.sleep(0.002)
-        self.in_step = False
+        return np.arange(self.batch, dtype=np.int32)
+
+    def step_lanes_submit(self, **desc):
+        import numpy as np
+        assert self.inflight < 2
+        self._note("step", tuple((k, tuple(np.asarray(v).ravel().tolist())) for k, v in sorted(desc.items())))
+        self.inflight += 1
+
+    def step_lanes_collect(self):
+        import numpy as np
+        assert self.inflight > 0
+        self.inflight -= 1
         return np.arange(self.batch, dtype=np.int32)
 
     def step_timing(self):
@@ -136,11 +144,12 @@ def _effects(log):
 
 
 def test_pipelined_live_loop_makes_the_sequential_loops_device_calls():
-    """workload.PipelinedLive plans step n+1 while step n runs on its worker
-    thread, then applies step n+1's fills, copies and primes: per step the
-    device receives the same effects and descriptors as from the sequential
-    loop (LiveDevice), none of them while a step is running, through
-    admissions, retirements and value-based evictions."""
+    """workload.PipelinedLive plans step n+1 while step n is in flight, then
+    applies step n+1's fills, copies and primes and submits it before
+    collecting step n: per step the device's stream receives the same effects
+    and descriptors as from the sequential loop (LiveDevice), with at most two
+    steps in flight, through admissions, retirements and value-based
+    evictions."""
     from rstr.workload import LiveDevice, PipelinedLive
     kw = dict(batch=6, page_size=16, physical_pages=60, maxpos=192, seed=11, arrival_mean=1.5,
               prompt=(8, 60), output=(2, 12), retain_finished=True)
@@ -156,6 +165,7 @@ def test_pipelined_live_loop_makes_the_sequential_loops_device_calls():
     for _ in range(n - 1):
         loop.step()
     loop.finish()
+    assert pip_dev.inflight == 0 and loop.inflight == 0
     assert pl.retired > 0 and pl.evicted > 0
     a, b = _effects(seq_dev.log), _effects(pip_dev.log)
     assert len(a) == len(b) == n
@@ -164,10 +174,10 @@ def test_pipelined_live_loop_makes_the_sequential_loops_device_calls():
         assert ea == eb, i
 
 
-def test_pipelined_live_loop_error_waits_for_the_running_step_and_restores_the_interpreter():
-    """A failing step surfaces from the next PipelinedLive.step after the step
-    still running has finished; the switch interval is restored."""
-    import sys
+def test_pipelined_live_loop_error_collects_the_running_step():
+    """A step whose submission fails surfaces from PipelinedLive.step after the
+    step still in flight has been collected: nothing is left in flight on the
+    decoder."""
     from rstr.workload import PipelinedLive
 
     class Failing(_FakeDevice):
@@ -175,13 +185,11 @@ def test_pipelined_live_loop_error_waits_for_the_running_step_and_restores_the_i
             super().__init__(batch)
             self.steps = 0
 
-        def step_lanes(self, **desc):
+        def step_lanes_submit(self, **desc):
             self.steps += 1
-            out = super().step_lanes(**desc)
             if self.steps == 3:
                 raise RuntimeError("device step failed")
-            return out
-    before = sys.getswitchinterval()
+            super().step_lanes_submit(**desc)
     dev = Failing(6)
     pl = ChurnPlanner(CFG, batch=6, page_size=16, physical_pages=60, maxpos=192, seed=11, arrival_mean=1.5,
                       prompt=(8, 60), output=(2, 12))
@@ -190,6 +198,5 @@ def test_pipelined_live_loop_error_waits_for_the_running_step_and_restores_the_i
     with pytest.raises(RuntimeError, match="device step failed"):
         for _ in range(10):
             loop.step()
-    assert sys.getswitchinterval() == before
-    assert loop.fut is None and not dev.in_step
+    assert loop.inflight == 0 and dev.inflight == 0
     assert dev.steps == 3
