@@ -123,7 +123,8 @@ int rstr_model_export_linear(rstr_model* m, int32_t layer, int32_t role, void* w
 int rstr_pool_open(rstr_model* m, int32_t page_size, int32_t physical_pages, rstr_pool** out);
 int rstr_pool_close(rstr_pool* p);
 /* Replaces copy-page! (page_pool.clj:892-900): one physical page of every
- * slab and layer, ordered before later work on the session stream. */
+ * slab and layer, ordered before later work on the session stream.  Returns
+ * once queued (the arguments are staged; it runs after earlier work). */
 int rstr_pool_copy_page(rstr_pool* p, int32_t src_page, int32_t dst_page);
 /* Raw slab transfer of fp16 elements (gpu/upload! and gpu/download on a pool
  * buffer key, page_pool.clj:284-293; the chunk restore/export staging). */
@@ -133,7 +134,7 @@ int rstr_pool_download(rstr_pool* p, int32_t slab, int32_t layer, int64_t src_el
                        uint16_t* dst, int64_t elements);
 /* Synthetic N(0,1) fp16 K/V in every layer of the listed pages, keyed by
  * (seed, layer, slab, element): the stand-in for a restored prefix used by
- * throughput runs.  No reference counterpart. */
+ * throughput runs.  No reference counterpart.  Returns once queued. */
 int rstr_pool_fill_synthetic(rstr_pool* p, const int32_t* pages, int32_t n_pages, uint64_t seed);
 
 /* ---- durable chunk transfer --------------------------------------------------
@@ -190,7 +191,8 @@ int rstr_decoder_open(rstr_model* m, rstr_pool* p, int32_t batch, int32_t pages_
 int rstr_decoder_close(rstr_decoder* d);
 /* Replaces prime-lanes! -> upload-ranges! :r0 (paged_decoder.clj:462-471,
  * decoder_gpu.clj:1248-1271): the prescaled embedding of each token becomes
- * the lane's pending input row; other lanes keep their resident row. */
+ * the lane's pending input row; other lanes keep their resident row.
+ * Returns once queued, ordered before the next step on the session stream. */
 int rstr_prime_lanes(rstr_decoder* d, int32_t n, const int32_t* lanes, const int32_t* tokens);
 /* Replaces decode-row! input upload (decoder_gpu.clj:1158-1170): arbitrary
  * f32 rows [n][d_model] (the multimodal seam). */

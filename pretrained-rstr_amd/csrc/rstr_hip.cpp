@@ -86,6 +86,54 @@ struct rstr_model {
   int64_t weight_bytes = 0;
 };
 
+// Pinned host staging for the small int32 lists that page fills, page copies
+// and primes send to the device: a ring of slots, each reused only after its
+// previous copy has run (an event per slot).  A call returns once its
+// arguments are staged and its work is queued on the session's stream, so it
+// does not wait for steps submitted before it.
+struct HostRing {
+  static constexpr int N = 8;
+  int32_t* h[N] = {};
+  size_t cap[N] = {};
+  hipEvent_t ev[N] = {};
+  bool used[N] = {};
+  int next = 0;
+  // copy a[0..na) then b[0..nb) into a free slot
+  hipError_t stage(const int32_t* a, size_t na, const int32_t* b, size_t nb, int32_t** out, int* slot) {
+    const int k = next;
+    next = (next + 1) % N;
+    hipError_t e = hipSuccess;
+    if (used[k] && (e = hipEventSynchronize(ev[k])) != hipSuccess) return e;
+    used[k] = false;
+    if (!ev[k] && (e = hipEventCreateWithFlags(&ev[k], hipEventDisableTiming)) != hipSuccess) return e;
+    if (cap[k] < na + nb) {
+      if (h[k]) hipHostFree(h[k]);
+      h[k] = nullptr;
+      cap[k] = 0;
+      if ((e = hipHostMalloc((void**)&h[k], sizeof(int32_t) * std::max<size_t>(na + nb, 64))) != hipSuccess) return e;
+      cap[k] = std::max<size_t>(na + nb, 64);
+    }
+    if (na) std::memcpy(h[k], a, sizeof(int32_t) * na);
+    if (nb) std::memcpy(h[k] + na, b, sizeof(int32_t) * nb);
+    *out = h[k];
+    *slot = k;
+    return hipSuccess;
+  }
+  // the slot's copies are queued: it is free again once the stream passes here
+  hipError_t queued(int slot, hipStream_t st) {
+    used[slot] = true;
+    return hipEventRecord(ev[slot], st);
+  }
+  void release() {
+    for (int k = 0; k < N; k++) {
+      if (h[k]) hipHostFree(h[k]);
+      if (ev[k]) hipEventDestroy(ev[k]);
+      h[k] = nullptr;
+      ev[k] = nullptr;
+    }
+  }
+};
+
 struct rstr_pool {
   rstr_model* m = nullptr;
   int page_size = 0, physical_pages = 0;
@@ -94,6 +142,9 @@ struct rstr_pool {
   uint16_t** d_slabs = nullptr;
   int32_t* d_pairs = nullptr;
   int32_t* h_pairs = nullptr;             // pinned
+  HostRing ring;                          // staging of fill page lists and copy pairs
+  int32_t* d_fill = nullptr;              // page list of a synthetic fill
+  int fill_cap = 0;
   uint16_t* tmpl = nullptr;               // synthetic-prefix page templates
   uint64_t tmpl_seed = 0;
   bool tmpl_ready = false;
@@ -199,6 +250,7 @@ struct rstr_decoder {
   int32_t* h_tok_q[2] = {nullptr, nullptr};
   hipEvent_t ev_q[2] = {nullptr, nullptr};
   int q_first = 0, q_n = 0;
+  HostRing ring;  // staging of primed lanes and tokens
 };
 
 // ---------------------------------------------------------------------------
@@ -661,6 +713,8 @@ extern "C" int rstr_pool_close(rstr_pool* p) {
   hipFree(p->d_slabs);
   hipFree(p->d_pairs);
   hipHostFree(p->h_pairs);
+  if (p->d_fill) hipFree(p->d_fill);
+  p->ring.release();
   if (p->tmpl) hipFree(p->tmpl);
   if (p->stage) hipFree(p->stage);
   if (p->d_chunk_pages) hipFree(p->d_chunk_pages);
@@ -856,12 +910,14 @@ extern "C" int rstr_pool_copy_page(rstr_pool* p, int32_t src, int32_t dst) {
     return fail(s, RSTR_E_INVALID, "Page view does not name a pool page");
   if (src == dst) return RSTR_OK;
   HIPCHK(s, hipSetDevice(s->device));
-  HIPCHK(s, hipStreamSynchronize(s->stream));
-  p->h_pairs[0] = src;
-  p->h_pairs[1] = dst;
-  HIPCHK(s, hipMemcpyAsync(p->d_pairs, p->h_pairs, 2 * sizeof(int32_t), hipMemcpyHostToDevice, s->stream));
+  // queued in stream order (after every step submitted before it), not waited for
+  int32_t* h = nullptr;
+  int slot = 0;
+  const int32_t pair[2] = {src, dst};
+  HIPCHK(s, p->ring.stage(pair, 2, nullptr, 0, &h, &slot));
+  HIPCHK(s, hipMemcpyAsync(p->d_pairs, h, 2 * sizeof(int32_t), hipMemcpyHostToDevice, s->stream));
+  HIPCHK(s, p->ring.queued(slot, s->stream));
   HIPCHK(s, launch_copy_pages(s->stream, p->d_slabs, 2 * p->m->d.n_layers, p->page_elems, p->d_pairs, 1));
-  HIPCHK(s, hipStreamSynchronize(s->stream));
   return RSTR_OK;
 }
 
@@ -906,16 +962,24 @@ extern "C" int rstr_pool_fill_synthetic(rstr_pool* p, const int32_t* pages, int3
     if (pages[i] < 0 || pages[i] >= p->physical_pages) return fail(s, RSTR_E_INVALID, "page out of range");
   if (n == 0) return RSTR_OK;
   HIPCHK(s, hipSetDevice(s->device));
-  int32_t* d = nullptr;
-  HIPCHK(s, dmalloc(&d, n));
-  hipError_t e = ensure_templates(p, seed);
-  if (e == hipSuccess) e = hipMemcpy(d, pages, sizeof(int32_t) * n, hipMemcpyHostToDevice);
-  if (e == hipSuccess)
-    e = launch_fill_synthetic(s->stream, p->d_slabs, p->m->d.n_layers, p->page_elems, p->tmpl, d, n,
-                              seed);
-  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-  hipFree(d);
-  HIPCHK(s, e);
+  HIPCHK(s, ensure_templates(p, seed));
+  if (n > p->fill_cap) {  // grows rarely; freeing waits for the device
+    HIPCHK(s, hipStreamSynchronize(s->stream));
+    if (p->d_fill) hipFree(p->d_fill);
+    p->d_fill = nullptr;
+    p->fill_cap = 0;
+    const int cap = std::max(n, 1024);
+    HIPCHK(s, dmalloc(&p->d_fill, cap));
+    p->fill_cap = cap;
+  }
+  // queued in stream order (after every step submitted before it), not waited for
+  int32_t* h = nullptr;
+  int slot = 0;
+  HIPCHK(s, p->ring.stage(pages, n, nullptr, 0, &h, &slot));
+  HIPCHK(s, hipMemcpyAsync(p->d_fill, h, sizeof(int32_t) * n, hipMemcpyHostToDevice, s->stream));
+  HIPCHK(s, p->ring.queued(slot, s->stream));
+  HIPCHK(s, launch_fill_synthetic(s->stream, p->d_slabs, p->m->d.n_layers, p->page_elems, p->tmpl, p->d_fill, n,
+                                  seed));
   return RSTR_OK;
 }
 
@@ -942,6 +1006,7 @@ static void decoder_free(rstr_decoder* d) {
     if (d->h_tok_q[i]) hipHostFree(d->h_tok_q[i]);
     if (d->ev_q[i]) hipEventDestroy(d->ev_q[i]);
   }
+  d->ring.release();
   delete d;
 }
 
@@ -1117,11 +1182,14 @@ extern "C" int rstr_prime_lanes(rstr_decoder* d, int32_t n, const int32_t* lanes
       return fail(s, RSTR_E_INVALID, "token id out of range");
   if (n == 0) return RSTR_OK;
   HIPCHK(s, hipSetDevice(s->device));
-  HIPCHK(s, hipStreamSynchronize(s->stream));
-  HIPCHK(s, hipMemcpy(d->d_lanes, lanes, sizeof(int32_t) * n, hipMemcpyHostToDevice));
-  HIPCHK(s, hipMemcpy(d->d_tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice));
+  // queued in stream order (after every step submitted before it), not waited for
+  int32_t* h = nullptr;
+  int slot = 0;
+  HIPCHK(s, d->ring.stage(lanes, n, tokens, n, &h, &slot));
+  HIPCHK(s, hipMemcpyAsync(d->d_lanes, h, sizeof(int32_t) * n, hipMemcpyHostToDevice, s->stream));
+  HIPCHK(s, hipMemcpyAsync(d->d_tokens, h + n, sizeof(int32_t) * n, hipMemcpyHostToDevice, s->stream));
+  HIPCHK(s, d->ring.queued(slot, s->stream));
   HIPCHK(s, launch_gather_rows(s->stream, d->m->emb, d->m->d.d_model, d->d_lanes, d->d_tokens, n, d->r0));
-  HIPCHK(s, hipStreamSynchronize(s->stream));
   return RSTR_OK;
 }
 
