@@ -175,14 +175,15 @@ def _lane_desc(lengths, pps, ps=16):
 
 
 @pytest.mark.gpu
-def test_submitted_steps_equal_synchronous_steps():
+@pytest.mark.parametrize("graph", [True, False])
+def test_submitted_steps_equal_synchronous_steps(graph):
     """rstr_step_lanes_submit / _collect: two steps in flight, a prime and a
     page copy issued between submissions (they run after the submitted steps in
     stream order), then the tokens collected in submission order, equal the
     synchronous rstr_step_lanes sequence on a twin decoder, tokens and resident
     rows; a third submission and a collection with nothing in flight fail with
     a state error and leave the decoder usable."""
-    print("case submitted steps", flush=True)
+    print(f"case submitted steps graph={graph}", flush=True)
     batch, pps, maxpos, split = 3, 4, 64, 16
     steps = [[5, 9, 0], [6, 10, 0], [7, 11, 3]]
     with hip.Session(0) as sess:
@@ -191,7 +192,9 @@ def test_submitted_steps_equal_synchronous_steps():
         for _ in range(2):
             p = hip.Pool(m, 16, batch * pps)
             p.fill_synthetic(np.arange(batch * pps, dtype=np.int32), 5)
-            twins.append((p, hip.Decoder(m, p, batch, pps, maxpos, split)))
+            d = hip.Decoder(m, p, batch, pps, maxpos, split)
+            d.set_graph(graph)
+            twins.append((p, d))
         (p1, d1), (p2, d2) = twins
         for p, d in twins:
             d.prime_lanes([0, 1], [3, 17])
